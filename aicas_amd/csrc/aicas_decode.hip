@@ -1,0 +1,321 @@
+// C ABI of libaicas_decode.so: argument checking, launch planning and kernel dispatch.
+// The declarations and their reference counterparts are in include/aicas_decode.h.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/aicas_decode.h"
+#include "decode_attn.hpp"
+#include "kv_append.hpp"
+
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_last_error[0] = '\0';
+  return AICAS_OK;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(AICAS_ERR_LAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+int ilog2(int64_t x) {
+  int s = 0;
+  while ((int64_t{1} << s) < x) ++s;
+  return s;
+}
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+int elem_bytes(int32_t dt) { return dt == AICAS_DTYPE_FP8_E4M3 ? 1 : 2; }
+bool valid_dtype(int32_t dt) { return dt == AICAS_DTYPE_BF16 || dt == AICAS_DTYPE_FP16 || dt == AICAS_DTYPE_FP8_E4M3; }
+bool valid_head_dim(int32_t d) { return d == 16 || d == 32 || d == 64 || d == 128; }
+
+// Tokens one workgroup iteration covers (must match KVTraits / decode_attn_kernel).
+int tokens_per_iteration(int32_t kv_dtype, int32_t head_dim) {
+  const int eb = elem_bytes(kv_dtype);
+  const int vec = 16 / eb;
+  const int r = head_dim / vec;
+  const int rpw = aicas::kWave / r;
+  const int unroll = kv_dtype == AICAS_DTYPE_FP8_E4M3 ? 2 : 4;
+  return rpw * aicas::kWavesPerBlock * unroll;
+}
+
+// Checks shared by append and decode; fills the device-side layout.
+int make_layout(const aicas_kv_cache_t* c, int32_t batch, int32_t num_kv_heads, int32_t head_dim,
+                aicas::KVLayout& out) {
+  if (!c) return fail(AICAS_ERR_INVALID, "cache descriptor is NULL");
+  if (!c->k || !c->v) return fail(AICAS_ERR_INVALID, "cache K/V pointers must be non-NULL");
+  if (!valid_dtype(c->kv_dtype)) return fail(AICAS_ERR_UNSUPPORTED, "unknown kv_dtype %d", c->kv_dtype);
+  if (!aligned16(c->k) || !aligned16(c->v)) return fail(AICAS_ERR_INVALID, "cache K/V must be 16-byte aligned");
+  const int eb = elem_bytes(c->kv_dtype);
+  if ((c->stride_blk * eb) % 16 || (c->stride_h * eb) % 16 || (c->stride_t * eb) % 16)
+    return fail(AICAS_ERR_INVALID, "cache strides must be multiples of 16 bytes (got %lld, %lld, %lld elements)",
+                (long long)c->stride_blk, (long long)c->stride_h, (long long)c->stride_t);
+  if (c->stride_t < head_dim) return fail(AICAS_ERR_INVALID, "cache token stride %lld < head_dim %d",
+                                          (long long)c->stride_t, head_dim);
+  if (c->page_size <= 0) return fail(AICAS_ERR_INVALID, "page_size must be positive");
+  if (c->kv_dtype == AICAS_DTYPE_FP8_E4M3 && (!c->k_scale || !c->v_scale))
+    return fail(AICAS_ERR_INVALID, "fp8 caches need k_scale and v_scale");
+  out.k = c->k;
+  out.v = c->v;
+  out.k_scale = c->k_scale;
+  out.v_scale = c->v_scale;
+  out.stride_blk = c->stride_blk;
+  out.stride_h = c->stride_h;
+  out.stride_t = c->stride_t;
+  out.scale_stride_blk = c->scale_stride_blk;
+  out.scale_stride_h = c->scale_stride_h;
+  out.page_size = c->page_size;
+  if (c->block_table) {
+    if (!is_pow2(c->page_size)) return fail(AICAS_ERR_INVALID, "paged caches need a power-of-two page_size");
+    if (c->block_table_stride <= 0 || c->num_blocks <= 0)
+      return fail(AICAS_ERR_INVALID, "paged caches need block_table_stride > 0 and num_blocks > 0");
+    const int64_t mt = c->block_table_stride * c->page_size;
+    out.block_table = c->block_table;
+    out.block_table_stride = c->block_table_stride;
+    out.num_blocks = c->num_blocks;
+    out.max_tokens = static_cast<int32_t>(mt > INT32_MAX ? INT32_MAX : mt);
+  } else {
+    out.block_table = nullptr;
+    out.block_table_stride = 0;
+    out.num_blocks = batch;
+    out.max_tokens = c->page_size;
+  }
+  (void)num_kv_heads;
+  return AICAS_OK;
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Dispatch tables.
+
+template <int SRC, int KV>
+int launch_append_d(const aicas::AppendParams& p, int32_t batch, int32_t head_dim, hipStream_t s) {
+  const dim3 grid(batch), block(aicas::kBlockThreads);
+  switch (head_dim) {
+    case 16: hipLaunchKernelGGL((aicas::kv_append_kernel<SRC, KV, 16>), grid, block, 0, s, p); break;
+    case 32: hipLaunchKernelGGL((aicas::kv_append_kernel<SRC, KV, 32>), grid, block, 0, s, p); break;
+    case 64: hipLaunchKernelGGL((aicas::kv_append_kernel<SRC, KV, 64>), grid, block, 0, s, p); break;
+    case 128: hipLaunchKernelGGL((aicas::kv_append_kernel<SRC, KV, 128>), grid, block, 0, s, p); break;
+    default: return fail(AICAS_ERR_UNSUPPORTED, "head_dim %d not supported", head_dim);
+  }
+  return check_launch("aicas_kv_append");
+}
+
+template <int Q, int KV, int D, int G>
+void launch_decode_pg(const aicas::DecodeParams& p, bool paged, dim3 grid, hipStream_t s) {
+  const dim3 block(aicas::kBlockThreads);
+  if (paged) {
+    hipLaunchKernelGGL((aicas::decode_attn_kernel<Q, KV, D, G, true>), grid, block, 0, s, p);
+  } else {
+    hipLaunchKernelGGL((aicas::decode_attn_kernel<Q, KV, D, G, false>), grid, block, 0, s, p);
+  }
+}
+
+template <int Q, int KV, int D>
+int launch_decode_g(const aicas::DecodeParams& p, int g, bool paged, dim3 grid, hipStream_t s) {
+  switch (g) {
+    case 1: launch_decode_pg<Q, KV, D, 1>(p, paged, grid, s); break;
+    case 2: launch_decode_pg<Q, KV, D, 2>(p, paged, grid, s); break;
+    case 4: launch_decode_pg<Q, KV, D, 4>(p, paged, grid, s); break;
+    case 8: launch_decode_pg<Q, KV, D, 8>(p, paged, grid, s); break;
+    default: return fail(AICAS_ERR_UNSUPPORTED, "GQA group size %d not supported (1, 2, 4 or 8)", g);
+  }
+  return check_launch("aicas_decode_attention");
+}
+
+template <int Q, int KV>
+int launch_decode_d(const aicas::DecodeParams& p, int d, int g, bool paged, dim3 grid, hipStream_t s) {
+  switch (d) {
+    case 16: return launch_decode_g<Q, KV, 16>(p, g, paged, grid, s);
+    case 32: return launch_decode_g<Q, KV, 32>(p, g, paged, grid, s);
+    case 64: return launch_decode_g<Q, KV, 64>(p, g, paged, grid, s);
+    case 128: return launch_decode_g<Q, KV, 128>(p, g, paged, grid, s);
+    default: return fail(AICAS_ERR_UNSUPPORTED, "head_dim %d not supported", d);
+  }
+}
+
+struct Plan {
+  int32_t tokens_per_split;
+  int32_t num_splits;
+  size_t counter_off, ml_off, acc_off, bytes;
+};
+
+int plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+         int32_t max_seq_len, int32_t page_size, int32_t hint, Plan& pl) {
+  if (!valid_dtype(kv_dtype)) return fail(AICAS_ERR_UNSUPPORTED, "unknown kv_dtype %d", kv_dtype);
+  if (!valid_head_dim(head_dim)) return fail(AICAS_ERR_UNSUPPORTED, "head_dim %d not supported", head_dim);
+  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_seq_len < 0)
+    return fail(AICAS_ERR_INVALID, "batch/heads must be positive and max_seq_len non-negative");
+  const int tpi = tokens_per_iteration(kv_dtype, head_dim);
+  int64_t tps;
+  if (hint > 0) {
+    tps = ceil_div(hint, tpi) * tpi;
+  } else {
+    // Aim for about 2048 workgroups (8 per CU on 256 CUs) while keeping >= 2 iterations per split.
+    const int64_t pairs = int64_t{batch} * num_kv_heads;
+    const int64_t want_splits = ceil_div(2048, pairs);
+    tps = ceil_div(ceil_div(int64_t{max_seq_len > 0 ? max_seq_len : 1}, want_splits), tpi) * tpi;
+    if (tps < 2 * tpi) tps = 2 * tpi;
+  }
+  // A split may touch at most kMaxBlockEntries block-table entries.
+  if (page_size > 0) {
+    const int64_t cap = (int64_t{aicas::kMaxBlockEntries} - 1) * page_size / tpi * tpi;
+    if (cap >= tpi && tps > cap) tps = cap;
+  }
+  if (tps > (int64_t{1} << 30)) tps = int64_t{1} << 30;
+  const int64_t splits = max_seq_len > 0 ? ceil_div(max_seq_len, tps) : 1;
+  if (splits > 65535) return fail(AICAS_ERR_UNSUPPORTED, "too many splits (%lld)", (long long)splits);
+  pl.tokens_per_split = static_cast<int32_t>(tps);
+  pl.num_splits = static_cast<int32_t>(splits);
+  const size_t parts = size_t(batch) * num_q_heads * splits;
+  pl.counter_off = 0;
+  pl.ml_off = align_up(size_t(batch) * num_kv_heads * sizeof(int32_t), 256);
+  pl.acc_off = pl.ml_off + align_up(parts * 2 * sizeof(float), 256);
+  pl.bytes = pl.acc_off + align_up(parts * head_dim * sizeof(float), 256);
+  return AICAS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* aicas_last_error(void) { return g_last_error; }
+
+int32_t aicas_abi_version(void) { return AICAS_ABI_VERSION; }
+
+int aicas_kv_append(const aicas_kv_cache_t* cache, int32_t src_dtype, const void* k_src, int64_t k_stride_b,
+                    int64_t k_stride_h, int64_t k_stride_t, const void* v_src, int64_t v_stride_b,
+                    int64_t v_stride_h, int64_t v_stride_t, const int32_t* positions, int32_t* seq_lens_out,
+                    int32_t* status, int32_t batch, int32_t num_kv_heads, int32_t head_dim, int32_t n_new,
+                    hipStream_t stream) {
+  if (batch <= 0 || num_kv_heads <= 0 || n_new <= 0)
+    return fail(AICAS_ERR_INVALID, "batch, num_kv_heads and n_new must be positive");
+  if (!valid_head_dim(head_dim)) return fail(AICAS_ERR_UNSUPPORTED, "head_dim %d not supported", head_dim);
+  if (src_dtype != AICAS_DTYPE_BF16 && src_dtype != AICAS_DTYPE_FP16)
+    return fail(AICAS_ERR_UNSUPPORTED, "new K/V rows must be bf16 or fp16");
+  if (!k_src || !v_src || !positions) return fail(AICAS_ERR_INVALID, "k_src, v_src and positions must be non-NULL");
+  if (!aligned16(k_src) || !aligned16(v_src)) return fail(AICAS_ERR_INVALID, "new K/V rows must be 16-byte aligned");
+  if ((k_stride_b % 8) || (k_stride_h % 8) || (k_stride_t % 8) || (v_stride_b % 8) || (v_stride_h % 8) ||
+      (v_stride_t % 8))
+    return fail(AICAS_ERR_INVALID, "new K/V strides must be multiples of 8 elements");
+  aicas::AppendParams p{};
+  int rc = make_layout(cache, batch, num_kv_heads, head_dim, p.cache);
+  if (rc) return rc;
+  if (cache->kv_dtype != AICAS_DTYPE_FP8_E4M3 && cache->kv_dtype != src_dtype)
+    return fail(AICAS_ERR_UNSUPPORTED, "a 16-bit cache must have the dtype of the new rows");
+  p.k_src = k_src;
+  p.v_src = v_src;
+  p.k_src_stride_b = k_stride_b;
+  p.k_src_stride_h = k_stride_h;
+  p.k_src_stride_t = k_stride_t;
+  p.v_src_stride_b = v_stride_b;
+  p.v_src_stride_h = v_stride_h;
+  p.v_src_stride_t = v_stride_t;
+  p.positions = positions;
+  p.seq_lens_out = seq_lens_out;
+  p.status = status;
+  p.num_kv_heads = num_kv_heads;
+  p.n_new = n_new;
+  using namespace aicas;
+  if (src_dtype == kBF16) {
+    if (cache->kv_dtype == kFP8E4M3) return launch_append_d<kBF16, kFP8E4M3>(p, batch, head_dim, stream);
+    return launch_append_d<kBF16, kBF16>(p, batch, head_dim, stream);
+  }
+  if (cache->kv_dtype == kFP8E4M3) return launch_append_d<kFP16, kFP8E4M3>(p, batch, head_dim, stream);
+  return launch_append_d<kFP16, kFP16>(p, batch, head_dim, stream);
+}
+
+int aicas_decode_plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                      int32_t head_dim, int32_t max_seq_len, int32_t page_size, int32_t tokens_per_split_hint,
+                      int32_t* tokens_per_split, int32_t* num_splits, size_t* workspace_bytes) {
+  Plan pl{};
+  const int rc = plan(kv_dtype, batch, num_q_heads, num_kv_heads, head_dim, max_seq_len, page_size,
+                      tokens_per_split_hint, pl);
+  if (rc) return rc;
+  if (tokens_per_split) *tokens_per_split = pl.tokens_per_split;
+  if (num_splits) *num_splits = pl.num_splits;
+  if (workspace_bytes) *workspace_bytes = pl.bytes;
+  return ok();
+}
+
+int aicas_decode_attention(const aicas_kv_cache_t* cache, int32_t q_dtype, const void* q, int64_t q_stride_b,
+                           int64_t q_stride_h, void* out, int64_t out_stride_b, int64_t out_stride_h,
+                           const int32_t* seq_lens, int32_t uniform_len, int32_t max_seq_len, int32_t batch,
+                           int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, float sm_scale,
+                           int32_t tokens_per_split, void* workspace, size_t workspace_bytes, int32_t* status,
+                           hipStream_t stream) {
+  if (q_dtype != AICAS_DTYPE_BF16 && q_dtype != AICAS_DTYPE_FP16)
+    return fail(AICAS_ERR_UNSUPPORTED, "q must be bf16 or fp16");
+  if (!q || !out) return fail(AICAS_ERR_INVALID, "q and out must be non-NULL");
+  if (!aligned16(q) || (q_stride_b % 8) || (q_stride_h % 8))
+    return fail(AICAS_ERR_INVALID, "q must be 16-byte aligned with strides that are multiples of 8 elements");
+  if ((reinterpret_cast<uintptr_t>(out) & 1u) != 0) return fail(AICAS_ERR_INVALID, "out must be 2-byte aligned");
+  if (num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0)
+    return fail(AICAS_ERR_INVALID, "num_q_heads (%d) must be a multiple of num_kv_heads (%d)", num_q_heads,
+                num_kv_heads);
+  if (!seq_lens && uniform_len < 0) return fail(AICAS_ERR_INVALID, "uniform_len must be non-negative");
+  aicas::DecodeParams p{};
+  int rc = make_layout(cache, batch, num_kv_heads, head_dim, p.cache);
+  if (rc) return rc;
+  if (cache->kv_dtype != AICAS_DTYPE_FP8_E4M3 && cache->kv_dtype != q_dtype)
+    return fail(AICAS_ERR_UNSUPPORTED, "a 16-bit cache must have the dtype of q");
+  const int32_t bound = seq_lens ? max_seq_len : uniform_len;
+  Plan pl{};
+  rc = plan(cache->kv_dtype, batch, num_q_heads, num_kv_heads, head_dim, bound,
+            cache->block_table ? cache->page_size : 0, tokens_per_split, pl);
+  if (rc) return rc;
+  if (!workspace) return fail(AICAS_ERR_WORKSPACE, "workspace is NULL (%zu bytes needed)", pl.bytes);
+  if (workspace_bytes < pl.bytes)
+    return fail(AICAS_ERR_WORKSPACE, "workspace has %zu bytes, %zu needed", workspace_bytes, pl.bytes);
+  if (!aligned16(workspace)) return fail(AICAS_ERR_INVALID, "workspace must be 16-byte aligned");
+  char* ws = static_cast<char*>(workspace);
+  p.q = q;
+  p.q_stride_b = q_stride_b;
+  p.q_stride_h = q_stride_h;
+  p.out = out;
+  p.out_stride_b = out_stride_b;
+  p.out_stride_h = out_stride_h;
+  p.seq_lens = seq_lens;
+  p.uniform_len = uniform_len;
+  p.num_q_heads = num_q_heads;
+  p.num_kv_heads = num_kv_heads;
+  p.tokens_per_split = pl.tokens_per_split;
+  p.max_splits = pl.num_splits;
+  p.page_shift = cache->block_table ? ilog2(cache->page_size) : 0;
+  p.scale_log2 = sm_scale * 1.4426950408889634f;
+  p.ws_counter = reinterpret_cast<int32_t*>(ws + pl.counter_off);
+  p.ws_ml = reinterpret_cast<float*>(ws + pl.ml_off);
+  p.ws_acc = reinterpret_cast<float*>(ws + pl.acc_off);
+  p.status = status;
+  const int g = num_q_heads / num_kv_heads;
+  const dim3 grid(pl.num_splits, num_kv_heads, batch);
+  const bool paged = cache->block_table != nullptr;
+  using namespace aicas;
+  const int kv = cache->kv_dtype;
+  if (q_dtype == kBF16) {
+    if (kv == kFP8E4M3) return launch_decode_d<kBF16, kFP8E4M3>(p, head_dim, g, paged, grid, stream);
+    return launch_decode_d<kBF16, kBF16>(p, head_dim, g, paged, grid, stream);
+  }
+  if (kv == kFP8E4M3) return launch_decode_d<kFP16, kFP8E4M3>(p, head_dim, g, paged, grid, stream);
+  return launch_decode_d<kFP16, kFP16>(p, head_dim, g, paged, grid, stream);
+}
+
+}  // extern "C"

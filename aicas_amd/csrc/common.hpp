@@ -1,0 +1,144 @@
+// Shared device helpers for the KV-append and decode-attention kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace aicas {
+
+// Element types understood by the kernels. The numeric values are part of the C ABI.
+enum DType : int32_t { kBF16 = 0, kFP16 = 1, kFP8E4M3 = 2 };
+
+// Status bits that kernels OR into an optional device status word when they had to clamp an
+// out-of-range length, position or block id instead of touching memory they do not own.
+enum StatusBits : int32_t {
+  kStatusLenClamped = 1,      // seq_len exceeded what the cache (or the block table) can hold
+  kStatusBlockOutOfRange = 2, // a block-table entry was outside [0, num_blocks)
+  kStatusAppendOverflow = 4,  // an append position was outside the cache; the row was dropped
+};
+
+constexpr int kWave = 64;
+constexpr int kBlockThreads = 256;
+constexpr int kWavesPerBlock = kBlockThreads / kWave;
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float f16lo(uint32_t w) {
+  return static_cast<float>(__builtin_bit_cast(f16x2_t, w).x);
+}
+__device__ __forceinline__ float f16hi(uint32_t w) {
+  return static_cast<float>(__builtin_bit_cast(f16x2_t, w).y);
+}
+
+// Two 16-bit values packed in one dword -> two floats.
+template <int DT>
+__device__ __forceinline__ void unpack2(uint32_t w, float& lo, float& hi) {
+  if constexpr (DT == kBF16) {
+    lo = bf16lo(w);
+    hi = bf16hi(w);
+  } else {
+    lo = f16lo(w);
+    hi = f16hi(w);
+  }
+}
+
+// acc + a.lo*b.lo + a.hi*b.hi with both products exact (16-bit inputs) and fp32 accumulation.
+template <int DT>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+  if constexpr (DT == kBF16) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b),
+                                           acc, false);
+  } else {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b), acc, false);
+  }
+}
+
+// float -> bf16 bits, round to nearest even, NaN kept quiet (same rule as torch's float->bfloat16).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+template <int DT>
+__device__ __forceinline__ uint16_t from_f32(float f) {
+  if constexpr (DT == kBF16) {
+    return f32_to_bf16(f);
+  } else {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+  }
+}
+
+// OCP FP8 E4M3 ("e4m3fn": bias 7, no infinities, S.1111.111 is NaN, max finite 448).
+// Encoder: round to nearest even; |x| is expected to be <= 448 already (callers clamp), and
+// NaN maps to 0x7f with the sign kept.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t mag = u & 0x7fffffffu;
+  if (mag > 0x7f800000u) return sign | 0x7fu;
+  if (mag >= 0x43e00000u) return sign | 0x7eu;  // |x| >= 448
+  if (mag < 0x3c800000u) {
+    // |x| < 2^-6: subnormal range, value = m * 2^-9 with m in [0, 8]; m == 8 is the smallest normal.
+    const float scaled = __uint_as_float(mag) * 512.0f;  // exact (power-of-two scaling)
+    return sign | static_cast<uint32_t>(__builtin_rintf(scaled));  // rint = round half to even
+  }
+  const uint32_t exp = (mag >> 23) - 127u + 7u;  // in [1, 15]
+  const uint32_t man = mag & 0x7fffffu;
+  uint32_t m3 = man >> 20;
+  const uint32_t rem = man & 0xfffffu;
+  if (rem > 0x80000u || (rem == 0x80000u && (m3 & 1u))) m3 += 1u;
+  return sign | ((exp << 3) + m3);  // a mantissa carry rolls into the exponent field
+}
+
+// Cross-lane reductions inside aligned groups of N lanes (N <= 16, one DPP row), result in every lane.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+  if constexpr (N >= 2) x += dpp_f32<0xB1>(x);   // quad_perm [1,0,3,2]
+  if constexpr (N >= 4) x += dpp_f32<0x4E>(x);   // quad_perm [2,3,0,1]
+  if constexpr (N >= 8) x += dpp_f32<0x141>(x);  // row_half_mirror
+  if constexpr (N >= 16) x += dpp_f32<0x140>(x); // row_mirror
+  return x;
+}
+
+template <int N>
+__device__ __forceinline__ float group_max(float x) {
+  if constexpr (N >= 2) x = fmaxf(x, dpp_f32<0xB1>(x));
+  if constexpr (N >= 4) x = fmaxf(x, dpp_f32<0x4E>(x));
+  if constexpr (N >= 8) x = fmaxf(x, dpp_f32<0x141>(x));
+  if constexpr (N >= 16) x = fmaxf(x, dpp_f32<0x140>(x));
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Where a token's K/V row lives. Contiguous caches are the one-block-per-sequence case:
+// block id = batch index, page_size = capacity, and the token stride may be any multiple of 16 bytes.
+struct KVLayout {
+  void* k;
+  void* v;
+  float* k_scale;
+  float* v_scale;
+  const int32_t* block_table;  // nullptr for contiguous caches
+  int64_t block_table_stride;
+  int64_t num_blocks;
+  int64_t stride_blk;  // elements
+  int64_t stride_h;
+  int64_t stride_t;
+  int64_t scale_stride_blk;
+  int64_t scale_stride_h;
+  int32_t page_size;
+  int32_t max_tokens;  // tokens one sequence can hold: capacity, or block_table_stride * page_size
+};
+
+}  // namespace aicas

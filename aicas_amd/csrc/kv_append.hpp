@@ -1,0 +1,128 @@
+// KV append: write each sequence's new K/V rows into its cache at positions[b] .. positions[b]+n_new-1.
+//
+// Semantics follow the preallocated in-place append of the reference
+// (dujunbaoV1/evaluation_wrapper.py:84-100, index_copy_ of the new rows at the current length), which
+// is bitwise the same cache content as HF DynamicLayer.update's torch.cat
+// (transformers/cache_utils.py:127-146). For fp8 caches the rows are quantized on write with one fp32
+// scale per (token, kv-head): scale = amax/448, q = e4m3(clamp(x / scale, -448, 448)).
+//
+// One workgroup per sequence. Thread 0 reads positions[b] and, after every row is written, stores
+// positions[b] + n_new into seq_lens_out[b]; because one workgroup owns a sequence, seq_lens_out may alias
+// positions (an in-place length bump that a captured HIP graph can replay step after step).
+#pragma once
+
+#include "common.hpp"
+
+namespace aicas {
+
+struct AppendParams {
+  KVLayout cache;
+  const void* k_src;
+  const void* v_src;
+  int64_t k_src_stride_b, k_src_stride_h, k_src_stride_t;  // elements; the head_dim stride is 1
+  int64_t v_src_stride_b, v_src_stride_h, v_src_stride_t;
+  const int32_t* positions;
+  int32_t* seq_lens_out;
+  int32_t* status;
+  int32_t num_kv_heads;
+  int32_t n_new;
+};
+
+// Row offset (elements) of token t of sequence b, head h; returns false if the token has no slot.
+__device__ __forceinline__ bool append_row_offset(const KVLayout& c, int b, int h, int t, int64_t& row,
+                                                  int64_t& srow, int32_t* status) {
+  if (t < 0 || t >= c.max_tokens) {
+    if (status) atomicOr(status, kStatusAppendOverflow);
+    return false;
+  }
+  int64_t blk;
+  int tin;
+  if (c.block_table) {
+    blk = c.block_table[static_cast<int64_t>(b) * c.block_table_stride + t / c.page_size];
+    tin = t % c.page_size;
+    if (blk < 0 || blk >= c.num_blocks) {
+      if (status) atomicOr(status, kStatusBlockOutOfRange);
+      return false;
+    }
+  } else {
+    blk = b;
+    tin = t;
+  }
+  row = blk * c.stride_blk + h * c.stride_h + static_cast<int64_t>(tin) * c.stride_t;
+  srow = blk * c.scale_stride_blk + h * c.scale_stride_h + tin;
+  return true;
+}
+
+// SRC_DT: dtype of the incoming rows (bf16 or fp16). KV_DT: cache dtype (same as SRC_DT, or fp8).
+template <int SRC_DT, int KV_DT, int D>
+__global__ __launch_bounds__(kBlockThreads) void kv_append_kernel(AppendParams p) {
+  constexpr int VEC = 8;      // source elements per thread (16 bytes)
+  constexpr int R = D / VEC;  // threads per row
+  static_assert(R >= 1 && R <= 16, "a row must fit one DPP row");
+  constexpr int ROWS_PER_PASS = kBlockThreads / R;
+
+  __shared__ int32_t s_pos;
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  if (tid == 0) s_pos = p.positions[b];
+  __syncthreads();
+  const int pos = s_pos;
+
+  const int lane = tid % R;
+  const int rows_per_tensor = p.num_kv_heads * p.n_new;
+  const int rows_total = 2 * rows_per_tensor;
+  for (int r = tid / R; r < rows_total; r += ROWS_PER_PASS) {
+    const int which = r / rows_per_tensor;  // 0 = K, 1 = V
+    const int rr = r - which * rows_per_tensor;
+    const int h = rr / p.n_new;
+    const int j = rr - h * p.n_new;
+    const uint16_t* src;
+    if (which == 0) {
+      src = static_cast<const uint16_t*>(p.k_src) + b * p.k_src_stride_b + h * p.k_src_stride_h +
+            j * p.k_src_stride_t;
+    } else {
+      src = static_cast<const uint16_t*>(p.v_src) + b * p.v_src_stride_b + h * p.v_src_stride_h +
+            j * p.v_src_stride_t;
+    }
+    const uint4 x = *reinterpret_cast<const uint4*>(src + lane * VEC);
+    int64_t row = 0, srow = 0;
+    const bool ok = append_row_offset(p.cache, b, h, pos + j, row, srow, p.status);
+    if constexpr (KV_DT == kFP8E4M3) {
+      float f[VEC];
+      unpack2<SRC_DT>(x.x, f[0], f[1]);
+      unpack2<SRC_DT>(x.y, f[2], f[3]);
+      unpack2<SRC_DT>(x.z, f[4], f[5]);
+      unpack2<SRC_DT>(x.w, f[6], f[7]);
+      float amax = 0.0f;
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) amax = fmaxf(amax, fabsf(f[i]));
+      amax = group_max<R>(amax);  // every lane of the row takes part, so the DPP exchange is complete
+      const float scale = amax / 448.0f;
+      uint32_t packed[2] = {0u, 0u};
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        uint32_t code = 0u;
+        if (scale > 0.0f) {
+          const float y = fminf(fmaxf(f[i] / scale, -448.0f), 448.0f);
+          code = f32_to_e4m3(y);
+        }
+        packed[i / 4] |= code << (8 * (i % 4));
+      }
+      if (ok) {
+        uint8_t* dst = static_cast<uint8_t*>(which == 0 ? p.cache.k : p.cache.v) + row + lane * VEC;
+        *reinterpret_cast<uint2*>(dst) = make_uint2(packed[0], packed[1]);
+        if (lane == 0) (which == 0 ? p.cache.k_scale : p.cache.v_scale)[srow] = scale;
+      }
+    } else {
+      static_assert(KV_DT == SRC_DT, "16-bit caches store the incoming rows bit for bit");
+      if (ok) {
+        uint16_t* dst = static_cast<uint16_t*>(which == 0 ? p.cache.k : p.cache.v) + row + lane * VEC;
+        *reinterpret_cast<uint4*>(dst) = x;
+      }
+    }
+  }
+  __syncthreads();
+  if (tid == 0 && p.seq_lens_out) p.seq_lens_out[b] = pos + p.n_new;
+}
+
+}  // namespace aicas

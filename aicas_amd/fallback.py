@@ -1,0 +1,65 @@
+"""SDPA route for the attention calls that are not q_len=1 decode (prefill, masked or
+``output_attentions`` calls, CPU tensors).
+
+These calls are outside the decode path this package accelerates; like the reference
+(triton_qwen3vl/fallback.py:23-64, routing in triton_qwen3vl/backends.py:194-205, 249-260) they go to HF's
+``sdpa_attention_forward`` when transformers is importable, else to ``F.scaled_dot_product_attention`` over
+``repeat_kv``. The decode path never reaches this module: a decode call that the HIP kernel cannot serve
+fails loudly instead.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+
+def repeat_kv(hidden_states: torch.Tensor, n_rep: int) -> torch.Tensor:
+    """[B, Hkv, L, D] -> [B, Hkv*n_rep, L, D]; q head i reads kv head i // n_rep (fallback.py:7-12)."""
+    batch, num_key_value_heads, seq_len, head_dim = hidden_states.shape
+    if n_rep == 1:
+        return hidden_states
+    expanded = hidden_states[:, :, None, :, :].expand(batch, num_key_value_heads, n_rep, seq_len, head_dim)
+    return expanded.reshape(batch, num_key_value_heads * n_rep, seq_len, head_dim)
+
+
+def _load_sdpa_attention_forward():
+    try:
+        from transformers.integrations.sdpa_attention import sdpa_attention_forward
+    except Exception:
+        return None
+    return sdpa_attention_forward
+
+
+def sdpa_fallback(
+    module: torch.nn.Module,
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    attention_mask: torch.Tensor | None,
+    dropout: float = 0.0,
+    scaling: float | None = None,
+    is_causal: bool | None = None,
+    **kwargs,
+) -> tuple[torch.Tensor, None]:
+    if getattr(key, "_aicas_kv", None) is not None and not key._aicas_kv.dense:
+        raise RuntimeError(
+            "this KV cache is paged or fp8 and can only be read by the aicas decode kernel; "
+            "SDPA cannot consume it (decode with attention_mask=None, q_len=1)"
+        )
+    sdpa_attention_forward = _load_sdpa_attention_forward()
+    if sdpa_attention_forward is not None:
+        return sdpa_attention_forward(
+            module, query, key, value, attention_mask, dropout=dropout, scaling=scaling, is_causal=is_causal,
+            **kwargs,
+        )
+
+    if hasattr(module, "num_key_value_groups"):
+        key = repeat_kv(key, module.num_key_value_groups)
+        value = repeat_kv(value, module.num_key_value_groups)
+    is_causal = is_causal if is_causal is not None else getattr(module, "is_causal", True)
+    is_causal = query.shape[2] > 1 and attention_mask is None and is_causal
+    attn_output = F.scaled_dot_product_attention(
+        query, key, value, attn_mask=attention_mask, dropout_p=dropout, scale=scaling, is_causal=is_causal
+    )
+    return attn_output.transpose(1, 2).contiguous(), None

@@ -1,0 +1,297 @@
+"""Tensor-level wrappers around the C ABI: cache descriptors, KV append, decode attention, workspaces.
+
+All work is enqueued on torch's current HIP stream of the tensors' device; nothing here synchronises the
+host, so the calls can be captured in a HIP graph (``torch.cuda.CUDAGraph``) once the decode workspace has
+been reserved for the largest shape the graph will see.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import AicasError, KVCacheDesc, check
+
+_DTYPE_CODE = {
+    torch.bfloat16: _lib.DTYPE_BF16,
+    torch.float16: _lib.DTYPE_FP16,
+    torch.float8_e4m3fn: _lib.DTYPE_FP8_E4M3,
+}
+
+FP8_DTYPE = torch.float8_e4m3fn
+SUPPORTED_HEAD_DIMS = frozenset({16, 32, 64, 128})
+SUPPORTED_GROUP_SIZES = frozenset({1, 2, 4, 8})
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODE[dtype]
+    except KeyError:
+        raise AicasError(_lib.ERR_UNSUPPORTED, f"dtype {dtype} is not supported") from None
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+@dataclass
+class KVCacheView:
+    """Where the K/V rows of a cache live, in the form the kernels take (``aicas_kv_cache_t``).
+
+    Contiguous: ``k``/``v`` are ``[B, Hkv, capacity, D]`` (any strides that keep rows 16-byte aligned,
+    head_dim stride 1), ``block_table`` is None. Paged: ``k``/``v`` are pools ``[num_blocks, Hkv, page, D]``
+    and ``block_table`` is ``[B, max_blocks]`` int32. fp8 caches carry fp32 scales shaped like the rows
+    without the head_dim axis.
+    """
+
+    k: torch.Tensor
+    v: torch.Tensor
+    k_scale: torch.Tensor | None = None
+    v_scale: torch.Tensor | None = None
+    block_table: torch.Tensor | None = None
+
+    def __post_init__(self) -> None:
+        if self.k.shape != self.v.shape or self.k.dtype != self.v.dtype:
+            raise AicasError(_lib.ERR_INVALID, "K and V caches must have the same shape and dtype")
+        if self.k.dim() != 4:
+            raise AicasError(_lib.ERR_INVALID, "K/V caches must be 4-D")
+        if self.k.stride(3) != 1 or self.v.stride(3) != 1:
+            raise AicasError(_lib.ERR_INVALID, "K/V caches need a unit head_dim stride")
+        if self.k.stride() != self.v.stride():
+            raise AicasError(_lib.ERR_INVALID, "K and V caches must share strides")
+        if self.is_fp8:
+            if self.k_scale is None or self.v_scale is None:
+                raise AicasError(_lib.ERR_INVALID, "fp8 caches need k_scale and v_scale")
+            for s in (self.k_scale, self.v_scale):
+                if s.dtype != torch.float32 or s.dim() != 3 or s.stride(2) != 1:
+                    raise AicasError(_lib.ERR_INVALID, "fp8 scales must be float32 [blocks, Hkv, rows] with unit row stride")
+            if self.k_scale.stride() != self.v_scale.stride():
+                raise AicasError(_lib.ERR_INVALID, "k_scale and v_scale must share strides")
+        if self.block_table is not None:
+            bt = self.block_table
+            if bt.dtype != torch.int32 or bt.dim() != 2 or bt.stride(1) != 1:
+                raise AicasError(_lib.ERR_INVALID, "block_table must be int32 [B, max_blocks] with unit column stride")
+
+    @property
+    def is_fp8(self) -> bool:
+        return self.k.dtype == FP8_DTYPE
+
+    @property
+    def paged(self) -> bool:
+        return self.block_table is not None
+
+    @property
+    def num_kv_heads(self) -> int:
+        return self.k.shape[1]
+
+    @property
+    def head_dim(self) -> int:
+        return self.k.shape[3]
+
+    @property
+    def page_size(self) -> int:
+        return self.k.shape[2]
+
+    @property
+    def max_tokens(self) -> int:
+        """Tokens one sequence can hold."""
+        if self.paged:
+            return self.block_table.shape[1] * self.page_size
+        return self.k.shape[2]
+
+    @property
+    def device(self) -> torch.device:
+        return self.k.device
+
+    def desc(self) -> KVCacheDesc:
+        d = KVCacheDesc()
+        d.k = self.k.data_ptr()
+        d.v = self.v.data_ptr()
+        d.k_scale = _ptr(self.k_scale)
+        d.v_scale = _ptr(self.v_scale)
+        d.stride_blk = self.k.stride(0)
+        d.stride_h = self.k.stride(1)
+        d.stride_t = self.k.stride(2)
+        if self.k_scale is not None:
+            d.scale_stride_blk = self.k_scale.stride(0)
+            d.scale_stride_h = self.k_scale.stride(1)
+        d.page_size = self.k.shape[2]
+        d.kv_dtype = dtype_code(self.k.dtype)
+        if self.block_table is not None:
+            d.block_table = self.block_table.data_ptr()
+            d.block_table_stride = self.block_table.stride(0)
+            d.num_blocks = self.k.shape[0]
+            if self.block_table.shape[1] > self.block_table.stride(0):
+                raise AicasError(_lib.ERR_INVALID, "block_table rows overlap")
+        else:
+            d.num_blocks = self.k.shape[0]
+        return d
+
+
+def _check_rows(x: torch.Tensor, name: str) -> None:
+    if x.dim() != 4 or x.stride(3) != 1:
+        raise AicasError(_lib.ERR_INVALID, f"{name} must be [B, Hkv, n, D] with unit head_dim stride")
+
+
+def kv_append(
+    cache: KVCacheView,
+    k_new: torch.Tensor,
+    v_new: torch.Tensor,
+    positions: torch.Tensor,
+    seq_lens_out: torch.Tensor | None = None,
+    status: torch.Tensor | None = None,
+) -> None:
+    """Write ``k_new``/``v_new`` ``[B, Hkv, n, D]`` at ``positions[b] .. +n-1`` of each sequence.
+
+    ``seq_lens_out[b] = positions[b] + n`` is stored after the rows (it may be ``positions`` itself).
+    fp8 caches quantize on write with one fp32 scale per (token, kv head).
+    """
+    _check_rows(k_new, "k_new")
+    _check_rows(v_new, "v_new")
+    if k_new.shape != v_new.shape or k_new.dtype != v_new.dtype:
+        raise AicasError(_lib.ERR_INVALID, "k_new and v_new must match")
+    B, H, n, D = k_new.shape
+    if H != cache.num_kv_heads or D != cache.head_dim:
+        raise AicasError(_lib.ERR_INVALID, f"new rows {tuple(k_new.shape)} do not fit cache heads/head_dim")
+    if positions.dtype != torch.int32 or positions.numel() < B or not positions.is_contiguous():
+        raise AicasError(_lib.ERR_INVALID, "positions must be a contiguous int32 tensor with one entry per sequence")
+    if seq_lens_out is not None and (seq_lens_out.dtype != torch.int32 or not seq_lens_out.is_contiguous()):
+        raise AicasError(_lib.ERR_INVALID, "seq_lens_out must be a contiguous int32 tensor")
+    for t in (k_new, v_new, positions, seq_lens_out, status):
+        if t is not None and t.device != cache.device:
+            raise AicasError(_lib.ERR_INVALID, "all tensors must be on the cache's device")
+    desc = cache.desc()
+    check(
+        _lib.lib().aicas_kv_append(
+            ctypes.byref(desc), dtype_code(k_new.dtype),
+            k_new.data_ptr(), k_new.stride(0), k_new.stride(1), k_new.stride(2),
+            v_new.data_ptr(), v_new.stride(0), v_new.stride(1), v_new.stride(2),
+            positions.data_ptr(), _ptr(seq_lens_out), _ptr(status),
+            B, H, D, n, _stream(cache.device),
+        )
+    )
+
+
+@dataclass(frozen=True)
+class DecodePlan:
+    tokens_per_split: int
+    num_splits: int
+    workspace_bytes: int
+
+
+def decode_plan(
+    kv_dtype: torch.dtype,
+    batch: int,
+    num_q_heads: int,
+    num_kv_heads: int,
+    head_dim: int,
+    max_seq_len: int,
+    page_size: int = 0,
+    tokens_per_split: int = 0,
+) -> DecodePlan:
+    tps = ctypes.c_int32()
+    ns = ctypes.c_int32()
+    wb = ctypes.c_size_t()
+    check(
+        _lib.lib().aicas_decode_plan(
+            dtype_code(kv_dtype), batch, num_q_heads, num_kv_heads, head_dim, max_seq_len, page_size,
+            tokens_per_split, ctypes.byref(tps), ctypes.byref(ns), ctypes.byref(wb),
+        )
+    )
+    return DecodePlan(tps.value, ns.value, wb.value)
+
+
+class Workspace:
+    """Zero-initialised scratch for split partials and arrival counters, one per (device, stream).
+
+    The kernels leave the counters at zero after every launch, so the buffer is reused as is. It only grows;
+    call :meth:`reserve` before capturing a HIP graph so that no allocation happens during capture.
+    """
+
+    _pool: dict[tuple[int, int], torch.Tensor] = {}
+
+    @classmethod
+    def get(cls, device: torch.device, nbytes: int) -> torch.Tensor:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        key = (idx, torch.cuda.current_stream(device).cuda_stream)
+        buf = cls._pool.get(key)
+        if buf is None or buf.numel() < nbytes:
+            size = max(nbytes, 1 << 20)
+            if buf is not None:
+                size = max(size, 2 * buf.numel())
+            buf = torch.zeros(size, dtype=torch.uint8, device=device)
+            cls._pool[key] = buf
+        return buf
+
+    @classmethod
+    def reserve(cls, device: torch.device, nbytes: int) -> torch.Tensor:
+        return cls.get(device, nbytes)
+
+    @classmethod
+    def clear(cls) -> None:
+        cls._pool.clear()
+
+
+def decode_attention(
+    q: torch.Tensor,
+    cache: KVCacheView,
+    *,
+    sm_scale: float,
+    seq_lens: torch.Tensor | None = None,
+    max_seq_len: int | None = None,
+    out: torch.Tensor | None = None,
+    tokens_per_split: int = 0,
+    workspace: torch.Tensor | None = None,
+    status: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """q ``[B, Hq, 1, D]`` (or ``[B, Hq, D]``) -> out of the same shape, attending to each sequence's cache.
+
+    ``seq_lens`` (int32 ``[B]``, on device) gives per-sequence lengths and ``max_seq_len`` must bound them;
+    without ``seq_lens`` every sequence has ``max_seq_len`` tokens (default: the cache capacity).
+    """
+    squeeze = q.dim() == 3
+    q4 = q.unsqueeze(2) if squeeze else q
+    if q4.dim() != 4 or q4.shape[2] != 1 or q4.stride(3) != 1:
+        raise AicasError(_lib.ERR_INVALID, "q must be [B, Hq, 1, D] with unit head_dim stride")
+    B, Hq, _, D = q4.shape
+    Hkv = cache.num_kv_heads
+    if D != cache.head_dim:
+        raise AicasError(_lib.ERR_INVALID, f"q head_dim {D} != cache head_dim {cache.head_dim}")
+    if max_seq_len is None:
+        max_seq_len = cache.max_tokens
+    if seq_lens is not None:
+        if seq_lens.dtype != torch.int32 or seq_lens.numel() < B or not seq_lens.is_contiguous():
+            raise AicasError(_lib.ERR_INVALID, "seq_lens must be a contiguous int32 tensor with one entry per sequence")
+        if seq_lens.device != cache.device:
+            raise AicasError(_lib.ERR_INVALID, "seq_lens must be on the cache's device")
+    if q4.device != cache.device:
+        raise AicasError(_lib.ERR_INVALID, "q must be on the cache's device")
+    if out is None:
+        out = torch.empty((B, Hq, 1, D), dtype=q.dtype, device=q.device)
+    out4 = out.unsqueeze(2) if out.dim() == 3 else out
+    if out4.shape != (B, Hq, 1, D) or out4.stride(3) != 1 or out4.dtype != q.dtype:
+        raise AicasError(_lib.ERR_INVALID, "out must be [B, Hq, 1, D] in q's dtype with unit head_dim stride")
+    pl = decode_plan(
+        cache.k.dtype, B, Hq, Hkv, D, max_seq_len, cache.page_size if cache.paged else 0, tokens_per_split
+    )
+    if workspace is None:
+        workspace = Workspace.get(cache.device, pl.workspace_bytes)
+    desc = cache.desc()
+    check(
+        _lib.lib().aicas_decode_attention(
+            ctypes.byref(desc), dtype_code(q.dtype), q4.data_ptr(), q4.stride(0), q4.stride(1),
+            out4.data_ptr(), out4.stride(0), out4.stride(1),
+            _ptr(seq_lens), int(max_seq_len) if seq_lens is None else 0, int(max_seq_len), B,
+            Hq, Hkv, D, float(sm_scale),
+            pl.tokens_per_split, workspace.data_ptr(), workspace.numel(), _ptr(status),
+            _stream(cache.device),
+        )
+    )
+    return out

@@ -1,0 +1,140 @@
+/*
+ * aicas_decode.h — C ABI of libaicas_decode.so: KV-cache append and q_len=1 GQA decode attention for
+ * AMD Instinct MI355X (gfx950).
+ *
+ * Every entry point takes raw device pointers, element strides and an hipStream_t, and enqueues its work
+ * on that stream without any host synchronisation or device allocation, so the calls can be captured in a
+ * HIP graph. Return value: 0 on success, a nonzero AICAS_ERR_* code otherwise; aicas_last_error() then
+ * returns a message for the calling thread.
+ *
+ * Reference interfaces these entry points replace (paths relative to the Frun1na/AICAS tree; the
+ * transformers paths are transformers 5.15.0):
+ *   aicas_kv_append         <- DynamicLayer.update, transformers/cache_utils.py:127-146 (torch.cat append),
+ *                              called from Cache.update, transformers/cache_utils.py:1349-1381;
+ *                              InplaceDecodeCacheLayer.update, dujunbaoV1/evaluation_wrapper.py:84-100;
+ *                              GraphDecodeCacheLayer.update, dujunbaoV1/evaluation_wrapper.py:162-175;
+ *                              _append_to_paged_kv_cache, new KV cache/evaluation_wrapper.py:143-195
+ *                              (paged layout; fp8 e4m3 replaces the KIVI 2-bit codec).
+ *   aicas_decode_attention  <- _gqa_decode_attention_forward / _gqa_decode_attention_fwd,
+ *                              triton_qwen3vl/gqa_decode_attention.py:268-327 and :46-141;
+ *                              decode_q1_gqa_forward, dujunbaoV1/native_cuda_ops/decode_q1_gqa.cpp:73-95;
+ *                              _paged_kv_attention, new KV cache/evaluation_wrapper.py:248-265.
+ *   aicas_decode_plan       <- the launch-configuration choice, triton_qwen3vl/gqa_decode_attention.py:287-292.
+ *   aicas_last_error        <- the ValueError / TORCH_CHECK messages, gqa_decode_attention.py:282 and
+ *                              decode_q1_gqa.cpp:65-92.
+ */
+#ifndef AICAS_DECODE_H
+#define AICAS_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AICAS_ABI_VERSION 1
+
+/* Element types. */
+#define AICAS_DTYPE_BF16 0
+#define AICAS_DTYPE_FP16 1
+#define AICAS_DTYPE_FP8_E4M3 2 /* OCP e4m3 ("e4m3fn"), one fp32 scale per (token, kv head) */
+
+/* Return codes. */
+#define AICAS_OK 0
+#define AICAS_ERR_INVALID 1     /* null pointer, bad size, misaligned pointer or stride */
+#define AICAS_ERR_UNSUPPORTED 2 /* head_dim / group size / dtype combination not built */
+#define AICAS_ERR_WORKSPACE 3   /* workspace smaller than aicas_decode_plan asked for */
+#define AICAS_ERR_LAUNCH 4      /* the HIP runtime rejected the launch */
+
+/* Bits a kernel ORs into the optional device status word when it clamped instead of faulting. */
+#define AICAS_STATUS_LEN_CLAMPED 1
+#define AICAS_STATUS_BLOCK_OUT_OF_RANGE 2
+#define AICAS_STATUS_APPEND_OVERFLOW 4
+
+/*
+ * A KV cache. Two layouts share one description:
+ *  - contiguous: K and V are [B, Hkv, capacity, D] (any element strides that keep rows 16-byte aligned,
+ *    head_dim stride 1); block_table = NULL, page_size = capacity, num_blocks = B and stride_blk is the batch
+ *    stride. HF's [B, Hkv, L, D] tensors and views into a preallocated buffer both fit.
+ *  - paged: K and V are pools [num_blocks, Hkv, page_size, D]; block_table is [B, block_table_stride] int32
+ *    physical block ids; token t of sequence b lives in block block_table[b][t / page_size], row
+ *    t % page_size. page_size must be a power of two.
+ * For AICAS_DTYPE_FP8_E4M3, k_scale / v_scale hold one fp32 per (block, head, row):
+ * scale index = blk * scale_stride_blk + h * scale_stride_h + row. Dequantised value = code * scale.
+ */
+typedef struct aicas_kv_cache {
+  void* k;
+  void* v;
+  float* k_scale;
+  float* v_scale;
+  const int32_t* block_table;
+  int64_t block_table_stride;
+  int64_t num_blocks;
+  int64_t stride_blk;
+  int64_t stride_h;
+  int64_t stride_t;
+  int64_t scale_stride_blk;
+  int64_t scale_stride_h;
+  int32_t page_size;
+  int32_t kv_dtype;
+} aicas_kv_cache_t;
+
+/*
+ * Append n_new tokens per sequence: rows k_src[b, h, j, :] / v_src[b, h, j, :] (src_dtype bf16 or fp16,
+ * head_dim stride 1, strides in elements) go to token position positions[b] + j of sequence b. A 16-bit
+ * cache must have kv_dtype == src_dtype and receives the rows bit for bit; an fp8 cache receives
+ * e4m3(clamp(x / s, -448, 448)) with s = max|row| / 448 stored in k_scale / v_scale (s = 0 and all-zero
+ * codes for an all-zero row). If seq_lens_out is not NULL, seq_lens_out[b] = positions[b] + n_new is
+ * written after the rows; it may alias positions. A row whose position falls outside the cache is dropped
+ * and AICAS_STATUS_APPEND_OVERFLOW is ORed into *status (status may be NULL).
+ * Replaces: transformers/cache_utils.py:127-146; dujunbaoV1/evaluation_wrapper.py:84-100, :162-175;
+ * new KV cache/evaluation_wrapper.py:143-195.
+ */
+int aicas_kv_append(const aicas_kv_cache_t* cache, int32_t src_dtype, const void* k_src, int64_t k_stride_b,
+                    int64_t k_stride_h, int64_t k_stride_t, const void* v_src, int64_t v_stride_b,
+                    int64_t v_stride_h, int64_t v_stride_t, const int32_t* positions, int32_t* seq_lens_out,
+                    int32_t* status, int32_t batch, int32_t num_kv_heads, int32_t head_dim, int32_t n_new,
+                    hipStream_t stream);
+
+/*
+ * Launch plan for aicas_decode_attention: the token range per split (tokens_per_split_hint, or 0 to choose
+ * automatically), the number of splits covering max_seq_len, and the workspace size in bytes. The
+ * workspace must be zero-filled once when first allocated; the kernels leave it re-armed (zero arrival
+ * counters) after every launch. Two launches that may run concurrently need two workspaces.
+ * Replaces: triton_qwen3vl/gqa_decode_attention.py:287-292 (block size / warps choice).
+ */
+int aicas_decode_plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                      int32_t head_dim, int32_t max_seq_len, int32_t page_size, int32_t tokens_per_split_hint,
+                      int32_t* tokens_per_split, int32_t* num_splits, size_t* workspace_bytes);
+
+/*
+ * out[b, hq, :] = softmax(q[b, hq, :] . K[b, hq / G, t, :] * sm_scale over t < L_b) . V[b, hq / G, t, :],
+ * G = num_q_heads / num_kv_heads, L_b = seq_lens[b] (or uniform_len when seq_lens is NULL).
+ * q and out are [B, Hq, D] with element strides (head_dim stride 1) in q_dtype (bf16 or fp16); a 16-bit
+ * cache must have kv_dtype == q_dtype. max_seq_len must bound every L_b: longer sequences are clamped and
+ * AICAS_STATUS_LEN_CLAMPED is set. An empty sequence (L_b == 0) yields zeros. head_dim in {16, 32, 64, 128},
+ * G in {1, 2, 4, 8}. tokens_per_split as from aicas_decode_plan (0 = automatic).
+ * Replaces: triton_qwen3vl/gqa_decode_attention.py:46-141, :268-327; dujunbaoV1/native_cuda_ops/
+ * decode_q1_gqa.cpp:73-95; new KV cache/evaluation_wrapper.py:248-265.
+ */
+int aicas_decode_attention(const aicas_kv_cache_t* cache, int32_t q_dtype, const void* q, int64_t q_stride_b,
+                           int64_t q_stride_h, void* out, int64_t out_stride_b, int64_t out_stride_h,
+                           const int32_t* seq_lens, int32_t uniform_len, int32_t max_seq_len, int32_t batch,
+                           int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, float sm_scale,
+                           int32_t tokens_per_split, void* workspace, size_t workspace_bytes, int32_t* status,
+                           hipStream_t stream);
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* aicas_last_error(void);
+
+/* AICAS_ABI_VERSION of the loaded library. */
+int32_t aicas_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AICAS_DECODE_H */

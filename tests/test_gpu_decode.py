@@ -1,0 +1,258 @@
+"""Decode attention on the GPU through the C ABI against the CPU oracle.
+
+Tolerances: bf16/fp16 KV max-abs 2e-2 and rel 1e-2 against SDPA over repeat_kv on the same
+rounded inputs; fp8 KV 6e-2 against the oracle on the dequantised cache.
+"""
+
+import math
+
+import pytest
+import torch
+
+from aicas_amd import _lib, ops
+from aicas_amd.gqa_decode_attention import gqa_decode_attention
+from oracle import reference_path as ref
+
+pytestmark = pytest.mark.gpu
+
+ATOL_16 = 2e-2
+RTOL_16 = 1e-2
+ATOL_FP8 = 6e-2
+
+
+def _rand(shape, gen, dtype=torch.bfloat16, scale=1.0):
+    return (torch.randn(shape, generator=gen) * scale).to(dtype)
+
+
+def _close16(out, expect):
+    torch.testing.assert_close(out.float().cpu(), expect.float(), atol=ATOL_16, rtol=RTOL_16)
+
+
+def test_reference_decode_case_fp16(dev):
+    """The reference's own decode numerics test (test/test_qwen3vl_triton_patch.py:419-446, forward part):
+    seed 1, fp16, q [1,4,1,64], k/v [1,2,65,64], scale 64^-0.5, vs SDPA(repeat_kv), atol = rtol = 1e-2."""
+    torch.manual_seed(1)
+    q = torch.randn(1, 4, 1, 64, device=dev, dtype=torch.float16)
+    k = torch.randn(1, 2, 65, 64, device=dev, dtype=torch.float16)
+    v = torch.randn(1, 2, 65, 64, device=dev, dtype=torch.float16)
+    scale = 64 ** -0.5
+    out = gqa_decode_attention(q, k, v, sm_scale=scale, num_key_value_groups=2)
+    expect = ref.sdpa_decode(q.cpu().float(), k.cpu().float(), v.cpu().float(), scale, 2)
+    torch.testing.assert_close(out.float().cpu(), expect, atol=1e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [16, 32, 64, 128])
+@pytest.mark.parametrize("G", [1, 2, 4, 8])
+def test_decode_shapes(dev, dtype, D, G):
+    gen = torch.Generator().manual_seed(100 + D + G)
+    B, Hkv, L = 2, 2, 300
+    q = _rand((B, Hkv * G, 1, D), gen, dtype)
+    k = _rand((B, Hkv, L, D), gen, dtype)
+    v = _rand((B, Hkv, L, D), gen, dtype)
+    scale = 1.0 / math.sqrt(D)
+    out = gqa_decode_attention(q.to(dev), k.to(dev), v.to(dev), sm_scale=scale, num_key_value_groups=G)
+    _close16(out, ref.sdpa_decode(q, k, v, scale, G))
+    assert (out.float().cpu() - ref.decode_fp64(q, k, v, scale, G)).abs().max() < ATOL_16
+
+
+@pytest.mark.parametrize("L", [1, 2, 7, 63, 64, 65, 129, 1000, 4099])
+def test_decode_lengths(dev, L):
+    gen = torch.Generator().manual_seed(L)
+    B, Hkv, G, D = 3, 8, 2, 128
+    q = _rand((B, Hkv * G, 1, D), gen)
+    k = _rand((B, Hkv, L, D), gen)
+    v = _rand((B, Hkv, L, D), gen)
+    scale = D ** -0.5
+    out = gqa_decode_attention(q.to(dev), k.to(dev), v.to(dev), sm_scale=scale, num_key_value_groups=G)
+    _close16(out, ref.sdpa_decode(q, k, v, scale, G))
+    if L == 1:
+        # one key: the output is that key's V row exactly
+        assert torch.equal(out.cpu(), ref.repeat_kv(v, G))
+
+
+def test_split_count_invariance(dev):
+    gen = torch.Generator().manual_seed(5)
+    B, Hkv, G, D, L = 2, 8, 2, 128, 3000
+    q, k, v = _rand((B, 16, 1, D), gen), _rand((B, Hkv, L, D), gen), _rand((B, Hkv, L, D), gen)
+    view = ops.KVCacheView(k.to(dev), v.to(dev))
+    outs = []
+    for tps in (64, 128, 256, 448, 1024, 4096):
+        outs.append(ops.decode_attention(q.to(dev), view, sm_scale=D ** -0.5, tokens_per_split=tps).float().cpu())
+    expect = ref.sdpa_decode(q, k, v, D ** -0.5, G)
+    for o in outs:
+        _close16(o, expect)
+        # different split partitions only reorder fp32 sums: at most one bf16 rounding step apart
+        assert (o - outs[0]).abs().max() <= 2.0 ** -7 * outs[0].abs().max()
+
+
+def test_ragged_seq_lens(dev, status):
+    gen = torch.Generator().manual_seed(9)
+    B, Hkv, G, D, cap = 6, 8, 2, 128, 700
+    lens = [0, 1, 64, 333, 512, 700]
+    q = _rand((B, Hkv * G, 1, D), gen)
+    k = _rand((B, Hkv, cap, D), gen)
+    v = _rand((B, Hkv, cap, D), gen)
+    view = ops.KVCacheView(k.to(dev), v.to(dev))
+    sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    out = ops.decode_attention(q.to(dev), view, sm_scale=D ** -0.5, seq_lens=sl, max_seq_len=cap, status=status)
+    torch.cuda.synchronize()
+    out = out.float().cpu()
+    assert out[0].abs().max() == 0  # empty sequence -> zeros
+    expect = ref.ragged_decode(q[1:], [k[b, :, : lens[b]] for b in range(1, B)],
+                               [v[b, :, : lens[b]] for b in range(1, B)], D ** -0.5, G)
+    torch.testing.assert_close(out[1:], expect.float(), atol=ATOL_16, rtol=RTOL_16)
+    assert int(status.item()) == 0
+
+
+def test_len_beyond_bound_is_clamped_and_reported(dev, status):
+    gen = torch.Generator().manual_seed(2)
+    B, Hkv, D, cap = 2, 2, 64, 100
+    q = _rand((B, 4, 1, D), gen)
+    k = _rand((B, Hkv, cap, D), gen)
+    v = _rand((B, Hkv, cap, D), gen)
+    sl = torch.tensor([100, 5000], dtype=torch.int32, device=dev)
+    out = ops.decode_attention(q.to(dev), ops.KVCacheView(k.to(dev), v.to(dev)), sm_scale=0.125,
+                               seq_lens=sl, max_seq_len=cap, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) & _lib.STATUS_LEN_CLAMPED
+    _close16(out, ref.sdpa_decode(q, k, v, 0.125, 2))
+
+
+def test_strided_views_and_outputs(dev):
+    """K/V as views into a larger preallocated buffer (the HF cache's returned views) and a strided q."""
+    gen = torch.Generator().manual_seed(11)
+    B, Hkv, G, D, cap, L = 2, 8, 2, 128, 512, 301
+    kbuf = _rand((B, Hkv, cap, D), gen).to(dev)
+    vbuf = _rand((B, Hkv, cap, D), gen).to(dev)
+    qbig = _rand((B, 1, Hkv * G, D), gen).to(dev)
+    q = qbig.transpose(1, 2)  # [B, Hq, 1, D] non-contiguous
+    out = gqa_decode_attention(q, kbuf[:, :, :L], vbuf[:, :, :L], sm_scale=D ** -0.5, num_key_value_groups=G)
+    expect = ref.sdpa_decode(q.cpu(), kbuf[:, :, :L].cpu(), vbuf[:, :, :L].cpu(), D ** -0.5, G)
+    _close16(out, expect)
+
+
+def test_special_cases(dev):
+    D, G = 128, 2
+    gen = torch.Generator().manual_seed(3)
+    # all keys equal -> uniform weights -> mean of V
+    q = _rand((1, 16, 1, D), gen)
+    k = _rand((1, 8, 1, D), gen).expand(1, 8, 777, D).contiguous()
+    v = _rand((1, 8, 777, D), gen)
+    out = gqa_decode_attention(q.to(dev), k.to(dev), v.to(dev), sm_scale=D ** -0.5, num_key_value_groups=G)
+    mean_v = ref.repeat_kv(v.float().mean(dim=2, keepdim=True), G)
+    torch.testing.assert_close(out.float().cpu(), mean_v, atol=ATOL_16, rtol=RTOL_16)
+    # equal queries within a group -> identical outputs for both heads
+    q2 = q.clone()
+    q2[:, 1::2] = q2[:, 0::2]
+    k2 = _rand((1, 8, 2000, D), gen)
+    out2 = gqa_decode_attention(q2.to(dev), k2.to(dev), v[:, :, :1].expand(1, 8, 2000, D).contiguous().to(dev),
+                                sm_scale=D ** -0.5, num_key_value_groups=G)
+    assert torch.equal(out2[:, 0::2].cpu(), out2[:, 1::2].cpu())
+
+
+def test_planted_logit_across_splits(dev):
+    """One dominant key per head (logit >= 10 above the rest) far from split 0: the LSE merge must pick its
+    V row. Different split sizes put it in different splits."""
+    gen = torch.Generator().manual_seed(4)
+    B, Hkv, G, D, L = 1, 8, 2, 128, 20000
+    q = _rand((B, 16, 1, D), gen)
+    k = _rand((B, Hkv, L, D), gen)
+    v = _rand((B, Hkv, L, D), gen)
+    from aicas_amd.workloads import plant_keys
+
+    planted = plant_keys(k, q, gen, [L])
+    view = ops.KVCacheView(k.to(dev), v.to(dev))
+    expect = ref.sdpa_decode(q, k, v, D ** -0.5, G)
+    for tps in (128, 1024, 8192):
+        out = ops.decode_attention(q.to(dev), view, sm_scale=D ** -0.5, tokens_per_split=tps).float().cpu()
+        torch.testing.assert_close(out, expect.float(), atol=ATOL_16, rtol=RTOL_16)
+        for (_, j, p, _) in planted:
+            # e^-10 * 20000 ~ 0.9 of mass elsewhere at worst; check the planted row dominates
+            w = out[0, j * G, 0]
+            assert torch.nn.functional.cosine_similarity(w, v[0, j, p].float(), dim=0) > 0.5
+
+
+@pytest.mark.parametrize("src_scale", [1.0])
+def test_paged_fp8_decode(dev, status, src_scale):
+    gen = torch.Generator().manual_seed(55)
+    B, Hkv, G, D, page = 5, 8, 2, 128, 16
+    lens = [1, 16, 17, 900, 2050]
+    per_seq = max((L + page - 1) // page for L in lens)
+    nblocks = B * per_seq
+    bt = torch.randperm(nblocks, generator=gen).to(torch.int32).view(B, per_seq)
+    src_k = _rand((nblocks, Hkv, page, D), gen, scale=src_scale)
+    src_v = _rand((nblocks, Hkv, page, D), gen, scale=src_scale)
+    ck, sk = ref.fp8_quantize_rows(src_k)
+    cv, sv = ref.fp8_quantize_rows(src_v)
+    q = _rand((B, Hkv * G, 1, D), gen)
+    view = ops.KVCacheView(ck.to(dev), cv.to(dev), sk.to(dev), sv.to(dev), bt.to(dev))
+    sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    out = ops.decode_attention(q.to(dev), view, sm_scale=D ** -0.5, seq_lens=sl, max_seq_len=max(lens),
+                               status=status).float().cpu()
+    torch.cuda.synchronize()
+    deq_k = ref.fp8_dequantize_rows(ck, sk)
+    deq_v = ref.fp8_dequantize_rows(cv, sv)
+    ks = ref.paged_gather(deq_k, bt, lens)
+    vs = ref.paged_gather(deq_v, bt, lens)
+    expect = ref.ragged_decode(q.float(), ks, vs, D ** -0.5, G)
+    assert (out - expect).abs().max() < ATOL_FP8
+    # Against the unquantised source the fp8 bar holds once the rounding errors of many rows average out
+    # (lengths >= 256, the range of the paged fp8 workload). A 1-token sequence returns one V row whose
+    # e4m3 rounding alone is up to 2^-4 relative per element, above any fixed absolute bar.
+    ks0 = ref.paged_gather(src_k.float(), bt, lens)
+    vs0 = ref.paged_gather(src_v.float(), bt, lens)
+    full = ref.ragged_decode(q.float(), ks0, vs0, D ** -0.5, G)
+    long_rows = [b for b, L in enumerate(lens) if L >= 256]
+    assert (out[long_rows] - full[long_rows]).abs().max() < ATOL_FP8
+    assert int(status.item()) == 0
+
+
+def test_paged_bf16_decode(dev):
+    gen = torch.Generator().manual_seed(56)
+    B, Hkv, G, D, page = 3, 8, 2, 128, 16
+    lens = [5, 300, 1111]
+    per_seq = max((L + page - 1) // page for L in lens)
+    nblocks = B * per_seq + 7
+    bt = torch.randperm(nblocks, generator=gen)[: B * per_seq].to(torch.int32).view(B, per_seq)
+    pk = _rand((nblocks, Hkv, page, D), gen)
+    pv = _rand((nblocks, Hkv, page, D), gen)
+    q = _rand((B, Hkv * G, 1, D), gen)
+    view = ops.KVCacheView(pk.to(dev), pv.to(dev), block_table=bt.to(dev))
+    sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    out = ops.decode_attention(q.to(dev), view, sm_scale=D ** -0.5, seq_lens=sl, max_seq_len=max(lens))
+    expect = ref.ragged_decode(q, ref.paged_gather(pk, bt, lens), ref.paged_gather(pv, bt, lens), D ** -0.5, G)
+    _close16(out, expect)
+
+
+def test_invalid_block_ids_are_skipped_and_reported(dev, status):
+    B, Hkv, D, page = 1, 2, 64, 16
+    pk = torch.randn((4, Hkv, page, D)).to(torch.bfloat16)
+    bt = torch.tensor([[0, 99, -3, 1]], dtype=torch.int32)
+    view = ops.KVCacheView(pk.to(dev), pk.clone().to(dev), block_table=bt.to(dev))
+    q = torch.randn((B, 4, 1, D)).to(torch.bfloat16)
+    sl = torch.tensor([64], dtype=torch.int32, device=dev)
+    out = ops.decode_attention(q.to(dev), view, sm_scale=0.125, seq_lens=sl, max_seq_len=64, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) & _lib.STATUS_BLOCK_OUT_OF_RANGE
+    # only blocks 0 and 1 (tokens 0..15 and 48..63) are visible
+    keys = torch.cat([pk[0], pk[1]], dim=1)[None]
+    _close16(out, ref.sdpa_decode(q, keys, keys, 0.125, 2))
+
+
+def test_fp8_code_decode_matches_table(dev):
+    """Every e4m3 code through the kernel's hardware conversion: a cache whose row is all 1.0-scaled codes,
+    a query that selects one position, so out = code value. Checks the gfx950 fp8 conversion is OCP."""
+    D = 16
+    table = ref.e4m3_decode_table()
+    finite = torch.tensor([c for c in range(256) if not math.isnan(table[c])], dtype=torch.int32)
+    B = finite.numel()
+    # sequence b holds one token whose every element is code finite[b]; with one key the output is that
+    # V row exactly (every e4m3 value is representable in bf16)
+    rows = finite.to(torch.uint8).view(B, 1, 1, 1).expand(B, 1, 1, D).contiguous().view(ops.FP8_DTYPE)
+    ones = torch.ones((B, 1, 1), dtype=torch.float32)
+    view = ops.KVCacheView(rows.to(dev), rows.clone().to(dev), ones.to(dev), ones.clone().to(dev))
+    q = torch.zeros((B, 1, 1, D), dtype=torch.bfloat16)
+    out = ops.decode_attention(q.to(dev), view, sm_scale=1.0).float().cpu()
+    expect = table[finite.long()].view(B, 1, 1, 1).expand(B, 1, 1, D)
+    assert torch.equal(out, expect)
