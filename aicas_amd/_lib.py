@@ -18,7 +18,7 @@ import torch  # noqa: F401  (must precede the library load, see above)
 LIB_NAME = "libaicas_decode.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_BF16 = 0
 DTYPE_FP16 = 1
@@ -39,6 +39,7 @@ EXPORTED_SYMBOLS = (
     "aicas_kv_append",
     "aicas_decode_plan",
     "aicas_decode_attention",
+    "aicas_decode_attention_append",
     "aicas_last_error",
     "aicas_abi_version",
 )
@@ -105,8 +106,18 @@ def _bind(handle: ctypes.CDLL) -> ctypes.CDLL:
     handle.aicas_decode_attention.argtypes = [
         ctypes.POINTER(KVCacheDesc), _I32, _P, _I64, _I64,
         _P, _I64, _I64,
-        _P, _I32, _I32, _I32,
+        _P, _I32, _I32, _I32, _I32,
         _I32, _I32, _I32, ctypes.c_float,
+        _I32, _P, _SIZE, _P,
+        _P,
+    ]
+    handle.aicas_decode_attention_append.restype = ctypes.c_int
+    handle.aicas_decode_attention_append.argtypes = [
+        ctypes.POINTER(KVCacheDesc), _I32, _P, _I64, _I64,
+        _P, _I64, _I64, _P, _I64, _I64,
+        _P, _I64, _I64,
+        _P, _P, _I32, _I32,
+        _I32, _I32, _I32, _I32, ctypes.c_float,
         _I32, _P, _SIZE, _P,
         _P,
     ]

@@ -15,14 +15,16 @@ import sys
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
-SOURCES = [os.path.join(CSRC, "aicas_decode.hip")]
-HEADERS = [
-    os.path.join(CSRC, "common.hpp"),
-    os.path.join(CSRC, "kv_append.hpp"),
-    os.path.join(CSRC, "decode_attn.hpp"),
-    os.path.join(os.path.dirname(PKG_DIR), "include", "aicas_decode.h"),
+SOURCES = [
+    os.path.join(CSRC, "aicas_decode.hip"),
+    os.path.join(CSRC, "decode_bf16_bf16.hip"),
+    os.path.join(CSRC, "decode_fp16_fp16.hip"),
+    os.path.join(CSRC, "decode_bf16_fp8.hip"),
+    os.path.join(CSRC, "decode_fp16_fp8.hip"),
 ]
+INCLUDE = os.path.join(os.path.dirname(PKG_DIR), "include")
 OUTPUT = os.path.join(PKG_DIR, "libaicas_decode.so")
+OBJ_DIR = os.path.join(PKG_DIR, "_build")
 ARCH = "gfx950"
 
 
@@ -32,26 +34,26 @@ def hipcc() -> str:
     return path if os.path.exists(path) else "hipcc"
 
 
-def command(output: str = OUTPUT) -> list[str]:
-    return [
-        hipcc(),
-        f"--offload-arch={ARCH}",
-        "-O3",
-        "-std=c++17",
-        "-fPIC",
-        "-shared",
-        "-mcode-object-version=5",
-        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        "-Wall",
-        "-o", output,
-        *SOURCES,
-    ]
+COMMON_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-mcode-object-version=5",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+]
 
 
-def build(verbose: bool = True) -> str:
-    """Compile the library in-tree (always recompiles) and return its path."""
-    tmp = OUTPUT + ".tmp"
-    cmd = command(tmp)
+def compile_command(source: str, obj: str, include: str = INCLUDE) -> list[str]:
+    return [hipcc(), *COMMON_FLAGS, "-I", include, "-c", "-o", obj, source]
+
+
+def link_command(objs: list[str], output: str) -> list[str]:
+    return [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", output, *objs]
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print("[aicas build]", " ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -61,8 +63,23 @@ def build(verbose: bool = True) -> str:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
     if err.strip() and verbose:
         print(err, file=sys.stderr)
-    os.replace(tmp, OUTPUT)
-    return OUTPUT
+
+
+def build(verbose: bool = True, sources: list[str] | None = None, output: str = OUTPUT,
+          include: str = INCLUDE, obj_dir: str = OBJ_DIR) -> str:
+    """Compile every translation unit in parallel and link the library in-tree (always recompiles)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    sources = sources or SOURCES
+    os.makedirs(obj_dir, exist_ok=True)
+    objs = [os.path.join(obj_dir, os.path.splitext(os.path.basename(src))[0] + ".o") for src in sources]
+    jobs = max(1, min(len(sources), os.cpu_count() or 1, 8))
+    with ThreadPoolExecutor(jobs) as pool:
+        list(pool.map(lambda so: _run(compile_command(so[0], so[1], include), verbose), zip(sources, objs)))
+    tmp = output + ".tmp"
+    _run(link_command(objs, tmp), verbose)
+    os.replace(tmp, output)
+    return output
 
 
 if __name__ == "__main__":

@@ -7,9 +7,16 @@
 #include <cstdio>
 #include <cstring>
 
-#include "../../include/aicas_decode.h"
+#include "aicas_decode.h"
 #include "decode_attn.hpp"
 #include "kv_append.hpp"
+
+// Decode launchers, one translation unit per (q dtype, kv dtype) pair (decode_<q>_<kv>.hip); they return
+// nonzero for a head_dim / group size that is not instantiated.
+int launch_decode_bf16_bf16(const aicas::DecodeParams&, int, int, bool, bool, dim3, hipStream_t);
+int launch_decode_fp16_fp16(const aicas::DecodeParams&, int, int, bool, bool, dim3, hipStream_t);
+int launch_decode_bf16_fp8(const aicas::DecodeParams&, int, int, bool, bool, dim3, hipStream_t);
+int launch_decode_fp16_fp8(const aicas::DecodeParams&, int, int, bool, bool, dim3, hipStream_t);
 
 namespace {
 
@@ -48,14 +55,10 @@ int elem_bytes(int32_t dt) { return dt == AICAS_DTYPE_FP8_E4M3 ? 1 : 2; }
 bool valid_dtype(int32_t dt) { return dt == AICAS_DTYPE_BF16 || dt == AICAS_DTYPE_FP16 || dt == AICAS_DTYPE_FP8_E4M3; }
 bool valid_head_dim(int32_t d) { return d == 16 || d == 32 || d == 64 || d == 128; }
 
-// Tokens one workgroup iteration covers (must match KVTraits / decode_attn_kernel).
+// Tokens one workgroup chunk covers (the kernel's own constant).
 int tokens_per_iteration(int32_t kv_dtype, int32_t head_dim) {
-  const int eb = elem_bytes(kv_dtype);
-  const int vec = 16 / eb;
-  const int r = head_dim / vec;
-  const int rpw = aicas::kWave / r;
-  const int unroll = kv_dtype == AICAS_DTYPE_FP8_E4M3 ? 2 : 4;
-  return rpw * aicas::kWavesPerBlock * unroll;
+  if (kv_dtype == AICAS_DTYPE_FP8_E4M3) return aicas::KVTraits<aicas::kFP8E4M3>::tokens_per_chunk(head_dim);
+  return aicas::KVTraits<aicas::kBF16>::tokens_per_chunk(head_dim);
 }
 
 // Checks shared by append and decode; fills the device-side layout.
@@ -119,43 +122,28 @@ int launch_append_d(const aicas::AppendParams& p, int32_t batch, int32_t head_di
   return check_launch("aicas_kv_append");
 }
 
-template <int Q, int KV, int D, int G>
-void launch_decode_pg(const aicas::DecodeParams& p, bool paged, dim3 grid, hipStream_t s) {
-  const dim3 block(aicas::kBlockThreads);
-  if (paged) {
-    hipLaunchKernelGGL((aicas::decode_attn_kernel<Q, KV, D, G, true>), grid, block, 0, s, p);
+template <bool APPEND>
+int launch_decode(const aicas::DecodeParams& p, int q_dtype, int kv_dtype, int d, int g, bool paged, dim3 grid,
+                  hipStream_t s) {
+  using namespace aicas;
+  int rc;
+  if (q_dtype == kBF16) {
+    rc = kv_dtype == kFP8E4M3 ? launch_decode_bf16_fp8(p, d, g, paged, APPEND, grid, s)
+                              : launch_decode_bf16_bf16(p, d, g, paged, APPEND, grid, s);
   } else {
-    hipLaunchKernelGGL((aicas::decode_attn_kernel<Q, KV, D, G, false>), grid, block, 0, s, p);
+    rc = kv_dtype == kFP8E4M3 ? launch_decode_fp16_fp8(p, d, g, paged, APPEND, grid, s)
+                              : launch_decode_fp16_fp16(p, d, g, paged, APPEND, grid, s);
   }
+  if (rc) return fail(AICAS_ERR_UNSUPPORTED, "head_dim %d / GQA group size %d not supported", d, g);
+  return check_launch(APPEND ? "aicas_decode_attention_append" : "aicas_decode_attention");
 }
 
-template <int Q, int KV, int D>
-int launch_decode_g(const aicas::DecodeParams& p, int g, bool paged, dim3 grid, hipStream_t s) {
-  switch (g) {
-    case 1: launch_decode_pg<Q, KV, D, 1>(p, paged, grid, s); break;
-    case 2: launch_decode_pg<Q, KV, D, 2>(p, paged, grid, s); break;
-    case 4: launch_decode_pg<Q, KV, D, 4>(p, paged, grid, s); break;
-    case 8: launch_decode_pg<Q, KV, D, 8>(p, paged, grid, s); break;
-    default: return fail(AICAS_ERR_UNSUPPORTED, "GQA group size %d not supported (1, 2, 4 or 8)", g);
-  }
-  return check_launch("aicas_decode_attention");
-}
-
-template <int Q, int KV>
-int launch_decode_d(const aicas::DecodeParams& p, int d, int g, bool paged, dim3 grid, hipStream_t s) {
-  switch (d) {
-    case 16: return launch_decode_g<Q, KV, 16>(p, g, paged, grid, s);
-    case 32: return launch_decode_g<Q, KV, 32>(p, g, paged, grid, s);
-    case 64: return launch_decode_g<Q, KV, 64>(p, g, paged, grid, s);
-    case 128: return launch_decode_g<Q, KV, 128>(p, g, paged, grid, s);
-    default: return fail(AICAS_ERR_UNSUPPORTED, "head_dim %d not supported", d);
-  }
-}
+constexpr int64_t kTargetWorkgroups = 448;
 
 struct Plan {
   int32_t tokens_per_split;
   int32_t num_splits;
-  size_t counter_off, ml_off, acc_off, bytes;
+  size_t counter_off, arrive_off, ml_off, acc_off, bytes;
 };
 
 int plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
@@ -169,9 +157,11 @@ int plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int32_t num_kv_he
   if (hint > 0) {
     tps = ceil_div(hint, tpi) * tpi;
   } else {
-    // Aim for about 2048 workgroups (8 per CU on 256 CUs) while keeping >= 2 iterations per split.
+    // Aim for about kTargetWorkgroups workgroups in total (measured on MI355X for the 28-layer B=8 L=2048
+    // decode: fewer leave HBM idle during each workgroup's start-up, more add split-merge traffic and a
+    // second round of workgroups), with at least two chunks per split.
     const int64_t pairs = int64_t{batch} * num_kv_heads;
-    const int64_t want_splits = ceil_div(2048, pairs);
+    const int64_t want_splits = ceil_div(kTargetWorkgroups, pairs);
     tps = ceil_div(ceil_div(int64_t{max_seq_len > 0 ? max_seq_len : 1}, want_splits), tpi) * tpi;
     if (tps < 2 * tpi) tps = 2 * tpi;
   }
@@ -187,10 +177,93 @@ int plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int32_t num_kv_he
   pl.num_splits = static_cast<int32_t>(splits);
   const size_t parts = size_t(batch) * num_q_heads * splits;
   pl.counter_off = 0;
-  pl.ml_off = align_up(size_t(batch) * num_kv_heads * sizeof(int32_t), 256);
+  pl.arrive_off = align_up(size_t(batch) * num_kv_heads * sizeof(int32_t), 256);
+  pl.ml_off = pl.arrive_off + align_up(size_t(batch) * sizeof(int32_t), 256);
   pl.acc_off = pl.ml_off + align_up(parts * 2 * sizeof(float), 256);
   pl.bytes = pl.acc_off + align_up(parts * head_dim * sizeof(float), 256);
   return AICAS_OK;
+}
+
+
+struct DecodeCall {
+  const aicas_kv_cache_t* cache;
+  int32_t q_dtype;
+  const void* q;
+  int64_t q_stride_b, q_stride_h;
+  void* out;
+  int64_t out_stride_b, out_stride_h;
+  const int32_t* lens;
+  int32_t uniform_len;
+  int32_t bound;
+  int32_t batch, num_q_heads, num_kv_heads, head_dim;
+  float sm_scale;
+  int32_t tokens_per_split;
+  void* workspace;
+  size_t workspace_bytes;
+  int32_t* status;
+  const void* k_new;
+  const void* v_new;
+  int64_t kn_stride_b, kn_stride_h, vn_stride_b, vn_stride_h;
+  int32_t* seq_lens_out;
+  int32_t min_len;
+};
+
+template <bool APPEND>
+int run_decode(const DecodeCall& c, hipStream_t stream) {
+  if (c.q_dtype != AICAS_DTYPE_BF16 && c.q_dtype != AICAS_DTYPE_FP16)
+    return fail(AICAS_ERR_UNSUPPORTED, "q must be bf16 or fp16");
+  if (!c.q || !c.out) return fail(AICAS_ERR_INVALID, "q and out must be non-NULL");
+  if (!aligned16(c.q) || (c.q_stride_b % 8) || (c.q_stride_h % 8))
+    return fail(AICAS_ERR_INVALID, "q must be 16-byte aligned with strides that are multiples of 8 elements");
+  if ((reinterpret_cast<uintptr_t>(c.out) & 1u) != 0) return fail(AICAS_ERR_INVALID, "out must be 2-byte aligned");
+  if (c.num_kv_heads <= 0 || c.num_q_heads % c.num_kv_heads != 0)
+    return fail(AICAS_ERR_INVALID, "num_q_heads (%d) must be a multiple of num_kv_heads (%d)", c.num_q_heads,
+                c.num_kv_heads);
+  aicas::DecodeParams p{};
+  int rc = make_layout(c.cache, c.batch, c.num_kv_heads, c.head_dim, p.cache);
+  if (rc) return rc;
+  if (c.cache->kv_dtype != AICAS_DTYPE_FP8_E4M3 && c.cache->kv_dtype != c.q_dtype)
+    return fail(AICAS_ERR_UNSUPPORTED, "a 16-bit cache must have the dtype of q");
+  Plan pl{};
+  rc = plan(c.cache->kv_dtype, c.batch, c.num_q_heads, c.num_kv_heads, c.head_dim, c.bound,
+            c.cache->block_table ? c.cache->page_size : 0, c.tokens_per_split, pl);
+  if (rc) return rc;
+  if (!c.workspace) return fail(AICAS_ERR_WORKSPACE, "workspace is NULL (%zu bytes needed)", pl.bytes);
+  if (c.workspace_bytes < pl.bytes)
+    return fail(AICAS_ERR_WORKSPACE, "workspace has %zu bytes, %zu needed", c.workspace_bytes, pl.bytes);
+  if (!aligned16(c.workspace)) return fail(AICAS_ERR_INVALID, "workspace must be 16-byte aligned");
+  char* ws = static_cast<char*>(c.workspace);
+  p.q = c.q;
+  p.q_stride_b = c.q_stride_b;
+  p.q_stride_h = c.q_stride_h;
+  p.out = c.out;
+  p.out_stride_b = c.out_stride_b;
+  p.out_stride_h = c.out_stride_h;
+  p.seq_lens = c.lens;
+  p.uniform_len = c.uniform_len;
+  p.num_q_heads = c.num_q_heads;
+  p.num_kv_heads = c.num_kv_heads;
+  p.tokens_per_split = pl.tokens_per_split;
+  p.max_splits = pl.num_splits;
+  p.page_shift = c.cache->block_table ? ilog2(c.cache->page_size) : 0;
+  p.scale_log2 = c.sm_scale * 1.4426950408889634f;
+  p.ws_counter = reinterpret_cast<int32_t*>(ws + pl.counter_off);
+  p.ws_arrive = reinterpret_cast<int32_t*>(ws + pl.arrive_off);
+  p.ws_ml = reinterpret_cast<float*>(ws + pl.ml_off);
+  p.ws_acc = reinterpret_cast<float*>(ws + pl.acc_off);
+  p.status = c.status;
+  p.k_new = c.k_new;
+  p.v_new = c.v_new;
+  p.kn_stride_b = c.kn_stride_b;
+  p.kn_stride_h = c.kn_stride_h;
+  p.vn_stride_b = c.vn_stride_b;
+  p.vn_stride_h = c.vn_stride_h;
+  p.seq_lens_out = c.seq_lens_out;
+  p.spec_len = c.min_len > 0 ? c.min_len : 0;
+  const int g = c.num_q_heads / c.num_kv_heads;
+  const dim3 grid(pl.num_splits, c.num_kv_heads, c.batch);
+  return launch_decode<APPEND>(p, c.q_dtype, c.cache->kv_dtype, c.head_dim, g, c.cache->block_table != nullptr,
+                               grid, stream);
 }
 
 }  // namespace
@@ -258,64 +331,80 @@ int aicas_decode_plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int3
 
 int aicas_decode_attention(const aicas_kv_cache_t* cache, int32_t q_dtype, const void* q, int64_t q_stride_b,
                            int64_t q_stride_h, void* out, int64_t out_stride_b, int64_t out_stride_h,
-                           const int32_t* seq_lens, int32_t uniform_len, int32_t max_seq_len, int32_t batch,
-                           int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, float sm_scale,
-                           int32_t tokens_per_split, void* workspace, size_t workspace_bytes, int32_t* status,
-                           hipStream_t stream) {
-  if (q_dtype != AICAS_DTYPE_BF16 && q_dtype != AICAS_DTYPE_FP16)
-    return fail(AICAS_ERR_UNSUPPORTED, "q must be bf16 or fp16");
-  if (!q || !out) return fail(AICAS_ERR_INVALID, "q and out must be non-NULL");
-  if (!aligned16(q) || (q_stride_b % 8) || (q_stride_h % 8))
-    return fail(AICAS_ERR_INVALID, "q must be 16-byte aligned with strides that are multiples of 8 elements");
-  if ((reinterpret_cast<uintptr_t>(out) & 1u) != 0) return fail(AICAS_ERR_INVALID, "out must be 2-byte aligned");
-  if (num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0)
-    return fail(AICAS_ERR_INVALID, "num_q_heads (%d) must be a multiple of num_kv_heads (%d)", num_q_heads,
-                num_kv_heads);
+                           const int32_t* seq_lens, int32_t uniform_len, int32_t min_len, int32_t max_seq_len,
+                           int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                           float sm_scale, int32_t tokens_per_split, void* workspace, size_t workspace_bytes,
+                           int32_t* status, hipStream_t stream) {
   if (!seq_lens && uniform_len < 0) return fail(AICAS_ERR_INVALID, "uniform_len must be non-negative");
-  aicas::DecodeParams p{};
-  int rc = make_layout(cache, batch, num_kv_heads, head_dim, p.cache);
-  if (rc) return rc;
-  if (cache->kv_dtype != AICAS_DTYPE_FP8_E4M3 && cache->kv_dtype != q_dtype)
-    return fail(AICAS_ERR_UNSUPPORTED, "a 16-bit cache must have the dtype of q");
-  const int32_t bound = seq_lens ? max_seq_len : uniform_len;
-  Plan pl{};
-  rc = plan(cache->kv_dtype, batch, num_q_heads, num_kv_heads, head_dim, bound,
-            cache->block_table ? cache->page_size : 0, tokens_per_split, pl);
-  if (rc) return rc;
-  if (!workspace) return fail(AICAS_ERR_WORKSPACE, "workspace is NULL (%zu bytes needed)", pl.bytes);
-  if (workspace_bytes < pl.bytes)
-    return fail(AICAS_ERR_WORKSPACE, "workspace has %zu bytes, %zu needed", workspace_bytes, pl.bytes);
-  if (!aligned16(workspace)) return fail(AICAS_ERR_INVALID, "workspace must be 16-byte aligned");
-  char* ws = static_cast<char*>(workspace);
-  p.q = q;
-  p.q_stride_b = q_stride_b;
-  p.q_stride_h = q_stride_h;
-  p.out = out;
-  p.out_stride_b = out_stride_b;
-  p.out_stride_h = out_stride_h;
-  p.seq_lens = seq_lens;
-  p.uniform_len = uniform_len;
-  p.num_q_heads = num_q_heads;
-  p.num_kv_heads = num_kv_heads;
-  p.tokens_per_split = pl.tokens_per_split;
-  p.max_splits = pl.num_splits;
-  p.page_shift = cache->block_table ? ilog2(cache->page_size) : 0;
-  p.scale_log2 = sm_scale * 1.4426950408889634f;
-  p.ws_counter = reinterpret_cast<int32_t*>(ws + pl.counter_off);
-  p.ws_ml = reinterpret_cast<float*>(ws + pl.ml_off);
-  p.ws_acc = reinterpret_cast<float*>(ws + pl.acc_off);
-  p.status = status;
-  const int g = num_q_heads / num_kv_heads;
-  const dim3 grid(pl.num_splits, num_kv_heads, batch);
-  const bool paged = cache->block_table != nullptr;
-  using namespace aicas;
-  const int kv = cache->kv_dtype;
-  if (q_dtype == kBF16) {
-    if (kv == kFP8E4M3) return launch_decode_d<kBF16, kFP8E4M3>(p, head_dim, g, paged, grid, stream);
-    return launch_decode_d<kBF16, kBF16>(p, head_dim, g, paged, grid, stream);
-  }
-  if (kv == kFP8E4M3) return launch_decode_d<kFP16, kFP8E4M3>(p, head_dim, g, paged, grid, stream);
-  return launch_decode_d<kFP16, kFP16>(p, head_dim, g, paged, grid, stream);
+  DecodeCall c{};
+  c.cache = cache;
+  c.q_dtype = q_dtype;
+  c.q = q;
+  c.q_stride_b = q_stride_b;
+  c.q_stride_h = q_stride_h;
+  c.out = out;
+  c.out_stride_b = out_stride_b;
+  c.out_stride_h = out_stride_h;
+  c.lens = seq_lens;
+  c.uniform_len = uniform_len;
+  c.min_len = seq_lens ? min_len : uniform_len;
+  c.bound = seq_lens ? max_seq_len : uniform_len;
+  c.batch = batch;
+  c.num_q_heads = num_q_heads;
+  c.num_kv_heads = num_kv_heads;
+  c.head_dim = head_dim;
+  c.sm_scale = sm_scale;
+  c.tokens_per_split = tokens_per_split;
+  c.workspace = workspace;
+  c.workspace_bytes = workspace_bytes;
+  c.status = status;
+  return run_decode<false>(c, stream);
+}
+
+int aicas_decode_attention_append(const aicas_kv_cache_t* cache, int32_t q_dtype, const void* q,
+                                  int64_t q_stride_b, int64_t q_stride_h, const void* k_new, int64_t k_stride_b,
+                                  int64_t k_stride_h, const void* v_new, int64_t v_stride_b, int64_t v_stride_h,
+                                  void* out, int64_t out_stride_b, int64_t out_stride_h, const int32_t* positions,
+                                  int32_t* seq_lens_out, int32_t min_len, int32_t max_seq_len, int32_t batch,
+                                  int32_t num_q_heads,
+                                  int32_t num_kv_heads, int32_t head_dim, float sm_scale, int32_t tokens_per_split,
+                                  void* workspace, size_t workspace_bytes, int32_t* status, hipStream_t stream) {
+  if (!positions) return fail(AICAS_ERR_INVALID, "positions must be non-NULL");
+  if (!k_new || !v_new) return fail(AICAS_ERR_INVALID, "k_new and v_new must be non-NULL");
+  if (!aligned16(k_new) || !aligned16(v_new) || (k_stride_b % 8) || (k_stride_h % 8) || (v_stride_b % 8) ||
+      (v_stride_h % 8))
+    return fail(AICAS_ERR_INVALID, "new K/V rows must be 16-byte aligned with strides that are multiples of 8");
+  if (max_seq_len < 1) return fail(AICAS_ERR_INVALID, "max_seq_len must count the appended token");
+  DecodeCall c{};
+  c.cache = cache;
+  c.q_dtype = q_dtype;
+  c.q = q;
+  c.q_stride_b = q_stride_b;
+  c.q_stride_h = q_stride_h;
+  c.out = out;
+  c.out_stride_b = out_stride_b;
+  c.out_stride_h = out_stride_h;
+  c.lens = positions;
+  c.uniform_len = 0;
+  c.min_len = min_len;
+  c.bound = max_seq_len;
+  c.batch = batch;
+  c.num_q_heads = num_q_heads;
+  c.num_kv_heads = num_kv_heads;
+  c.head_dim = head_dim;
+  c.sm_scale = sm_scale;
+  c.tokens_per_split = tokens_per_split;
+  c.workspace = workspace;
+  c.workspace_bytes = workspace_bytes;
+  c.status = status;
+  c.k_new = k_new;
+  c.v_new = v_new;
+  c.kn_stride_b = k_stride_b;
+  c.kn_stride_h = k_stride_h;
+  c.vn_stride_b = v_stride_b;
+  c.vn_stride_h = v_stride_h;
+  c.seq_lens_out = seq_lens_out;
+  return run_decode<true>(c, stream);
 }
 
 }  // extern "C"

@@ -34,8 +34,9 @@ class AicasKV:
 
     cache: ops.KVCacheView
     seq_lens: torch.Tensor      # int32 [B] on device, lengths after the latest append
-    max_seq_len: int            # host-side bound on seq_lens
+    max_seq_len: int            # host-side upper bound on seq_lens
     batch: int
+    min_seq_len: int = 0        # host-side lower bound on seq_lens
     workspace: torch.Tensor | None = None
     dense: bool = True          # the tensor itself is a [B, Hkv, L, D] view usable by other backends
 
@@ -117,7 +118,7 @@ def gqa_decode_attention(
     if meta is not None:
         return ops.decode_attention(
             q, meta.cache, sm_scale=sm_scale, seq_lens=meta.seq_lens, max_seq_len=meta.max_seq_len,
-            workspace=meta.workspace,
+            min_seq_len=meta.min_seq_len, workspace=meta.workspace,
         )
     k, v = key, value
     if not (_row_aligned(k) and _row_aligned(v) and k.stride() == v.stride()):

@@ -165,7 +165,7 @@ class AicasKVCacheLayer(CacheLayerMixin):
         contiguous16 = self.page_size is None and not self.view.is_fp8
         return AicasKV(
             cache=self.view, seq_lens=self.seq_lens, max_seq_len=max(self.host_lens), batch=self.batch,
-            workspace=workspace, dense=contiguous16 and uniform,
+            min_seq_len=min(self.host_lens), workspace=workspace, dense=contiguous16 and uniform,
         )
 
     def _result(self, key_states, value_states, n, was_empty):

@@ -246,6 +246,7 @@ def decode_attention(
     sm_scale: float,
     seq_lens: torch.Tensor | None = None,
     max_seq_len: int | None = None,
+    min_seq_len: int = 0,
     out: torch.Tensor | None = None,
     tokens_per_split: int = 0,
     workspace: torch.Tensor | None = None,
@@ -253,8 +254,10 @@ def decode_attention(
 ) -> torch.Tensor:
     """q ``[B, Hq, 1, D]`` (or ``[B, Hq, D]``) -> out of the same shape, attending to each sequence's cache.
 
-    ``seq_lens`` (int32 ``[B]``, on device) gives per-sequence lengths and ``max_seq_len`` must bound them;
-    without ``seq_lens`` every sequence has ``max_seq_len`` tokens (default: the cache capacity).
+    ``seq_lens`` (int32 ``[B]``, on device) gives per-sequence lengths; ``max_seq_len`` must bound them and
+    ``min_seq_len`` (optional) is a lower bound the caller guarantees, which lets the kernel start reading
+    K/V before it has read ``seq_lens``. Without ``seq_lens`` every sequence has ``max_seq_len`` tokens
+    (default: the cache capacity).
     """
     squeeze = q.dim() == 3
     q4 = q.unsqueeze(2) if squeeze else q
@@ -288,8 +291,74 @@ def decode_attention(
         _lib.lib().aicas_decode_attention(
             ctypes.byref(desc), dtype_code(q.dtype), q4.data_ptr(), q4.stride(0), q4.stride(1),
             out4.data_ptr(), out4.stride(0), out4.stride(1),
-            _ptr(seq_lens), int(max_seq_len) if seq_lens is None else 0, int(max_seq_len), B,
+            _ptr(seq_lens), int(max_seq_len) if seq_lens is None else 0, int(min_seq_len), int(max_seq_len), B,
             Hq, Hkv, D, float(sm_scale),
+            pl.tokens_per_split, workspace.data_ptr(), workspace.numel(), _ptr(status),
+            _stream(cache.device),
+        )
+    )
+    return out
+
+
+def decode_attention_append(
+    q: torch.Tensor,
+    cache: KVCacheView,
+    k_new: torch.Tensor,
+    v_new: torch.Tensor,
+    positions: torch.Tensor,
+    *,
+    sm_scale: float,
+    max_seq_len: int,
+    min_seq_len: int = 0,
+    seq_lens_out: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+    tokens_per_split: int = 0,
+    workspace: torch.Tensor | None = None,
+    status: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """One decode step in one launch: append ``k_new``/``v_new`` (``[B, Hkv, 1, D]`` or ``[B, Hkv, D]``) at
+    ``positions[b]`` and attend over ``positions[b] + 1`` tokens. ``seq_lens_out[b] = positions[b] + 1`` (it
+    may be ``positions`` itself). ``max_seq_len`` bounds ``positions[b] + 1``; ``min_seq_len`` (optional) is a
+    lower bound on every ``positions[b]``."""
+    squeeze = q.dim() == 3
+    q4 = q.unsqueeze(2) if squeeze else q
+    if q4.dim() != 4 or q4.shape[2] != 1 or q4.stride(3) != 1:
+        raise AicasError(_lib.ERR_INVALID, "q must be [B, Hq, 1, D] with unit head_dim stride")
+    B, Hq, _, D = q4.shape
+    kn = k_new.squeeze(2) if k_new.dim() == 4 else k_new
+    vn = v_new.squeeze(2) if v_new.dim() == 4 else v_new
+    if kn.shape != (B, cache.num_kv_heads, D) or vn.shape != kn.shape or kn.stride(2) != 1 or vn.stride(2) != 1:
+        raise AicasError(_lib.ERR_INVALID, "k_new/v_new must be [B, Hkv, 1, D] with unit head_dim stride")
+    if kn.dtype != q.dtype or vn.dtype != q.dtype:
+        raise AicasError(_lib.ERR_INVALID, "k_new/v_new must have q's dtype")
+    if D != cache.head_dim:
+        raise AicasError(_lib.ERR_INVALID, f"q head_dim {D} != cache head_dim {cache.head_dim}")
+    if positions.dtype != torch.int32 or positions.numel() < B or not positions.is_contiguous():
+        raise AicasError(_lib.ERR_INVALID, "positions must be a contiguous int32 tensor with one entry per sequence")
+    if seq_lens_out is not None and (seq_lens_out.dtype != torch.int32 or not seq_lens_out.is_contiguous()):
+        raise AicasError(_lib.ERR_INVALID, "seq_lens_out must be a contiguous int32 tensor")
+    for t in (q4, kn, vn, positions, seq_lens_out, status):
+        if t is not None and t.device != cache.device:
+            raise AicasError(_lib.ERR_INVALID, "all tensors must be on the cache's device")
+    if out is None:
+        out = torch.empty((B, Hq, 1, D), dtype=q.dtype, device=q.device)
+    out4 = out.unsqueeze(2) if out.dim() == 3 else out
+    if out4.shape != (B, Hq, 1, D) or out4.stride(3) != 1 or out4.dtype != q.dtype:
+        raise AicasError(_lib.ERR_INVALID, "out must be [B, Hq, 1, D] in q's dtype with unit head_dim stride")
+    pl = decode_plan(
+        cache.k.dtype, B, Hq, cache.num_kv_heads, D, max_seq_len, cache.page_size if cache.paged else 0,
+        tokens_per_split,
+    )
+    if workspace is None:
+        workspace = Workspace.get(cache.device, pl.workspace_bytes)
+    desc = cache.desc()
+    check(
+        _lib.lib().aicas_decode_attention_append(
+            ctypes.byref(desc), dtype_code(q.dtype), q4.data_ptr(), q4.stride(0), q4.stride(1),
+            kn.data_ptr(), kn.stride(0), kn.stride(1), vn.data_ptr(), vn.stride(0), vn.stride(1),
+            out4.data_ptr(), out4.stride(0), out4.stride(1),
+            positions.data_ptr(), _ptr(seq_lens_out), int(min_seq_len), int(max_seq_len),
+            B, Hq, cache.num_kv_heads, D, float(sm_scale),
             pl.tokens_per_split, workspace.data_ptr(), workspace.numel(), _ptr(status),
             _stream(cache.device),
         )

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define AICAS_ABI_VERSION 1
+#define AICAS_ABI_VERSION 2
 
 /* Element types. */
 #define AICAS_DTYPE_BF16 0
@@ -116,16 +116,42 @@ int aicas_decode_plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int3
  * q and out are [B, Hq, D] with element strides (head_dim stride 1) in q_dtype (bf16 or fp16); a 16-bit
  * cache must have kv_dtype == q_dtype. max_seq_len must bound every L_b: longer sequences are clamped and
  * AICAS_STATUS_LEN_CLAMPED is set. An empty sequence (L_b == 0) yields zeros. head_dim in {16, 32, 64, 128},
- * G in {1, 2, 4, 8}. tokens_per_split as from aicas_decode_plan (0 = automatic).
+ * G in {1, 2, 4, 8}. tokens_per_split as from aicas_decode_plan (0 = automatic). min_len is a lower bound on every
+ * L_b that the caller guarantees (0 if unknown; ignored when seq_lens is NULL): it lets contiguous-cache
+ * kernels start reading K/V before they have read seq_lens. A min_len above some L_b makes that sequence's
+ * result undefined (never out of bounds).
  * Replaces: triton_qwen3vl/gqa_decode_attention.py:46-141, :268-327; dujunbaoV1/native_cuda_ops/
  * decode_q1_gqa.cpp:73-95; new KV cache/evaluation_wrapper.py:248-265.
  */
 int aicas_decode_attention(const aicas_kv_cache_t* cache, int32_t q_dtype, const void* q, int64_t q_stride_b,
                            int64_t q_stride_h, void* out, int64_t out_stride_b, int64_t out_stride_h,
-                           const int32_t* seq_lens, int32_t uniform_len, int32_t max_seq_len, int32_t batch,
-                           int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, float sm_scale,
-                           int32_t tokens_per_split, void* workspace, size_t workspace_bytes, int32_t* status,
-                           hipStream_t stream);
+                           const int32_t* seq_lens, int32_t uniform_len, int32_t min_len, int32_t max_seq_len,
+                           int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                           float sm_scale, int32_t tokens_per_split, void* workspace, size_t workspace_bytes,
+                           int32_t* status, hipStream_t stream);
+
+/*
+ * One decode step of append + attend in a single launch: for every sequence b the new rows
+ * k_new[b, h, :] / v_new[b, h, :] ([B, Hkv, D], head_dim stride 1, dtype q_dtype) are written at token
+ * positions[b] of the cache exactly as aicas_kv_append would write them (fp8 caches quantize on write), and
+ * the attention runs over L_b = positions[b] + 1 tokens, the new one included, with the result
+ * aicas_kv_append followed by aicas_decode_attention would give. If seq_lens_out is not NULL,
+ * seq_lens_out[b] = positions[b] + 1 is stored once every workgroup has read positions[b]; it may alias
+ * positions. max_seq_len must bound positions[b] + 1; min_len (0 if unknown) is a lower bound on every
+ * positions[b], as for aicas_decode_attention. A token with no slot left in the cache is dropped and
+ * AICAS_STATUS_APPEND_OVERFLOW is set. The workspace must come from aicas_decode_plan with the same shapes.
+ * Replaces the pair Qwen3VLTextAttention.forward issues per layer and step
+ * (transformers/models/qwen3_vl/modeling_qwen3_vl.py:487-503): past_key_values.update (cache_utils.py:127-146)
+ * followed by the text attention function (triton_qwen3vl/backends.py:207-227).
+ */
+int aicas_decode_attention_append(const aicas_kv_cache_t* cache, int32_t q_dtype, const void* q,
+                                  int64_t q_stride_b, int64_t q_stride_h, const void* k_new, int64_t k_stride_b,
+                                  int64_t k_stride_h, const void* v_new, int64_t v_stride_b, int64_t v_stride_h,
+                                  void* out, int64_t out_stride_b, int64_t out_stride_h, const int32_t* positions,
+                                  int32_t* seq_lens_out, int32_t min_len, int32_t max_seq_len, int32_t batch,
+                                  int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, float sm_scale,
+                                  int32_t tokens_per_split, void* workspace, size_t workspace_bytes, int32_t* status,
+                                  hipStream_t stream);
 
 /* Message describing the last failure on the calling thread ("" if none). */
 const char* aicas_last_error(void);

@@ -256,3 +256,28 @@ def test_fp8_code_decode_matches_table(dev):
     out = ops.decode_attention(q.to(dev), view, sm_scale=1.0).float().cpu()
     expect = table[finite.long()].view(B, 1, 1, 1).expand(B, 1, 1, D)
     assert torch.equal(out, expect)
+
+
+@pytest.mark.parametrize("tps", [0, 64, 320])
+def test_min_seq_len_hint_gives_identical_results(dev, tps):
+    """A caller-guaranteed lower bound on the lengths only lets the kernel fetch early; results are unchanged."""
+    gen = torch.Generator().manual_seed(77)
+    B, Hkv, G, D, cap = 4, 8, 2, 128, 2300
+    lens = [2100, 2112, 2200, 2299]
+    q = _rand((B, Hkv * G, 1, D), gen).to(dev)
+    view = ops.KVCacheView(_rand((B, Hkv, cap, D), gen).to(dev), _rand((B, Hkv, cap, D), gen).to(dev))
+    sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    base = ops.decode_attention(q, view, sm_scale=D ** -0.5, seq_lens=sl, max_seq_len=cap, tokens_per_split=tps)
+    hinted = ops.decode_attention(q, view, sm_scale=D ** -0.5, seq_lens=sl, max_seq_len=cap, min_seq_len=min(lens),
+                                  tokens_per_split=tps)
+    assert torch.equal(base.cpu(), hinted.cpu())
+    kn = _rand((B, Hkv, 1, D), gen).to(dev)
+    pos_a = sl.clone()
+    view_b = ops.KVCacheView(view.k.clone(), view.v.clone())
+    pos_b = sl.clone()
+    fa = ops.decode_attention_append(q, view, kn, kn, pos_a, sm_scale=D ** -0.5, max_seq_len=cap, seq_lens_out=pos_a,
+                                     tokens_per_split=tps)
+    fb = ops.decode_attention_append(q, view_b, kn, kn, pos_b, sm_scale=D ** -0.5, max_seq_len=cap,
+                                     min_seq_len=min(lens), seq_lens_out=pos_b, tokens_per_split=tps)
+    assert torch.equal(fa.cpu(), fb.cpu())
+    assert torch.equal(view.k.cpu().view(torch.int16), view_b.k.cpu().view(torch.int16))
