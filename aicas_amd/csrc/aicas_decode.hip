@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
 
 #include "aicas_decode.h"
 #include "decode_attn.hpp"
@@ -55,10 +56,26 @@ int elem_bytes(int32_t dt) { return dt == AICAS_DTYPE_FP8_E4M3 ? 1 : 2; }
 bool valid_dtype(int32_t dt) { return dt == AICAS_DTYPE_BF16 || dt == AICAS_DTYPE_FP16 || dt == AICAS_DTYPE_FP8_E4M3; }
 bool valid_head_dim(int32_t d) { return d == 16 || d == 32 || d == 64 || d == 128; }
 
-// Tokens one workgroup chunk covers (the kernel's own constant).
+// Tokens one workgroup chunk covers, and the rows one workgroup load covers (the kernel's own constants).
 int tokens_per_iteration(int32_t kv_dtype, int32_t head_dim) {
   if (kv_dtype == AICAS_DTYPE_FP8_E4M3) return aicas::KVTraits<aicas::kFP8E4M3>::tokens_per_chunk(head_dim);
   return aicas::KVTraits<aicas::kBF16>::tokens_per_chunk(head_dim);
+}
+int rows_per_load(int32_t kv_dtype, int32_t head_dim) {
+  return tokens_per_iteration(kv_dtype, head_dim) / aicas::KVTraits<aicas::kBF16>::kUnroll;
+}
+
+// Compute units of the current device (queried once per device; 256 on MI355X).
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
 }
 
 // Checks shared by append and decode; fills the device-side layout.
@@ -138,7 +155,9 @@ int launch_decode(const aicas::DecodeParams& p, int q_dtype, int kv_dtype, int d
   return check_launch(APPEND ? "aicas_decode_attention_append" : "aicas_decode_attention");
 }
 
-constexpr int64_t kTargetWorkgroups = 448;
+// Workgroups per compute unit the split planner aims for, in quarters: 7/4 measured best on MI355X for the
+// 28-layer B=8 L=2048 decode (4 to 12 splits per (batch, kv head) pair within 7% of each other).
+constexpr int kWorkgroupsPerCUx4 = 7;
 
 struct Plan {
   int32_t tokens_per_split;
@@ -153,17 +172,18 @@ int plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int32_t num_kv_he
   if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_seq_len < 0)
     return fail(AICAS_ERR_INVALID, "batch/heads must be positive and max_seq_len non-negative");
   const int tpi = tokens_per_iteration(kv_dtype, head_dim);
+  const int rpb = rows_per_load(kv_dtype, head_dim);
   int64_t tps;
   if (hint > 0) {
-    tps = ceil_div(hint, tpi) * tpi;
+    tps = ceil_div(hint, rpb) * rpb;
   } else {
-    // Aim for about kTargetWorkgroups workgroups in total (measured on MI355X for the 28-layer B=8 L=2048
-    // decode: fewer leave HBM idle during each workgroup's start-up, more add split-merge traffic and a
-    // second round of workgroups), with at least two chunks per split.
+    // Split count: about kWorkgroupsPerCUx4 / 4 workgroups per compute unit in total.
     const int64_t pairs = int64_t{batch} * num_kv_heads;
-    const int64_t want_splits = ceil_div(kTargetWorkgroups, pairs);
-    tps = ceil_div(ceil_div(int64_t{max_seq_len > 0 ? max_seq_len : 1}, want_splits), tpi) * tpi;
-    if (tps < 2 * tpi) tps = 2 * tpi;
+    const int64_t target = int64_t{kWorkgroupsPerCUx4} * device_cus() / 4;
+    const int64_t splits_wanted = std::max<int64_t>(1, (target + pairs / 2) / pairs);
+    tps = ceil_div(int64_t{max_seq_len > 0 ? max_seq_len : 1}, splits_wanted);
+    tps = ceil_div(tps, rpb) * rpb;
+    if (tps < tpi) tps = tpi;
   }
   // A split may touch at most kMaxBlockEntries block-table entries.
   if (page_size > 0) {

@@ -29,9 +29,9 @@
 // L_b = positions[b] + 1 tokens, takes token L_b - 1 from the new rows (k_new / v_new) instead of the cache,
 // and the workgroup that owns that token writes the row into the cache (quantized on write for fp8 caches,
 // with the attention then using the dequantised row, exactly what a separate append followed by attention
-// would read). Every workgroup of batch row b counts itself in after reading positions[b]; the last one to
-// do so stores positions[b] + 1 to seq_lens_out[b] (which may alias positions), so no workgroup can read a
-// bumped length.
+// would read). Every workgroup of batch row b counts itself in when it exits (it read positions[b] at the
+// start); the last one to do so stores positions[b] + 1 to seq_lens_out[b] (which may alias positions), so
+// no workgroup can read a bumped length.
 #pragma once
 
 #include "common.hpp"
@@ -197,18 +197,23 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   if (tid == 0) s_len = p.seq_lens ? p.seq_lens[b] : p.uniform_len;
   __syncthreads();
   int L = s_len;
-  if constexpr (APPEND) {
-    // Count this workgroup in: thread 0's read of positions[b] has completed (its value went to LDS before
-    // the barrier); the last of the batch row's workgroups stores the bumped length.
-    if (tid == 0 && p.seq_lens_out) {
-      const int readers = gridDim.x * gridDim.y;
-      const int prev = __hip_atomic_fetch_add(p.ws_arrive + b, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (prev == readers - 1) {
-        p.seq_lens_out[b] = L + 1;
-        __hip_atomic_store(p.ws_arrive + b, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int len_read = L;
+  // APPEND with seq_lens_out: every workgroup counts itself in on its way out (thread 0's read of positions[b]
+  // completed long before: its value went to LDS ahead of the barrier above); the last of the batch row's
+  // workgroups stores the bumped length, so no workgroup can read it. Counting in at exit keeps the
+  // contended atomic off the start of the stream.
+  auto count_in = [&]() {
+    if constexpr (APPEND) {
+      if (tid == 0 && p.seq_lens_out) {
+        const int readers = gridDim.x * gridDim.y;
+        const int prev = __hip_atomic_fetch_add(p.ws_arrive + b, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (prev == readers - 1) {
+          p.seq_lens_out[b] = len_read + 1;
+          __hip_atomic_store(p.ws_arrive + b, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
     }
-  }
+  };
   if (L < 0) L = 0;
   int t_new = -1;  // APPEND: token served from the new rows
   if constexpr (APPEND) {
@@ -225,7 +230,10 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
     L = limit;
   }
   const int n_active = L > 0 ? (L + tps - 1) / tps : 1;
-  if (split >= n_active) return;
+  if (split >= n_active) {
+    count_in();
+    return;
+  }
   const int t_end = min(t_begin + tps, L);
 
   // Paged caches: stage this split's block ids in LDS (invalid ids become -1 and their tokens are skipped).
@@ -509,7 +517,10 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
       }
     }
   }
-  if (single) return;
+  if (single) {
+    count_in();
+    return;
+  }
 
   // Arrival: the partial stores above are complete (device-visible) before the counter moves.
   wait_vmem();
@@ -520,7 +531,10 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
     s_last = (prev == n_active - 1) ? 1 : 0;
   }
   __syncthreads();
-  if (!s_last) return;
+  if (!s_last) {
+    count_in();
+    return;
+  }
 
   // One online pass over the splits, MB at a time: the MB partials' loads are independent and in flight
   // together, so the merge costs about n_active / MB memory round trips.
@@ -555,6 +569,7 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
     outb[hq * p.out_stride_h + d] = from_f32<Q_DT>(ls > 0.0f ? a / ls : 0.0f);
   }
   if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  count_in();
 }
 
 }  // namespace aicas

@@ -64,27 +64,35 @@ __global__ __launch_bounds__(kBlockThreads) void kv_append_kernel(AppendParams p
   __shared__ int32_t s_pos;
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
+  const int lane = tid % R;
+  const int rows_per_tensor = p.num_kv_heads * p.n_new;
+  const int rows_total = 2 * rows_per_tensor;
+
+  // Source row r (K rows first, then V rows; head-major, then token).
+  auto src_row = [&](int r) -> const uint16_t* {
+    const int which = r / rows_per_tensor;
+    const int rr = r - which * rows_per_tensor;
+    const int h = rr / p.n_new;
+    const int j = rr - h * p.n_new;
+    return which == 0 ? static_cast<const uint16_t*>(p.k_src) + b * p.k_src_stride_b + h * p.k_src_stride_h +
+                            j * p.k_src_stride_t
+                      : static_cast<const uint16_t*>(p.v_src) + b * p.v_src_stride_b + h * p.v_src_stride_h +
+                            j * p.v_src_stride_t;
+  };
+  // The first pass's rows are loaded before the position is known, overlapping the two reads.
+  const int r0 = tid / R;
+  uint4 x_first = make_uint4(0u, 0u, 0u, 0u);
+  if (r0 < rows_total) x_first = *reinterpret_cast<const uint4*>(src_row(r0) + lane * VEC);
   if (tid == 0) s_pos = p.positions[b];
   __syncthreads();
   const int pos = s_pos;
 
-  const int lane = tid % R;
-  const int rows_per_tensor = p.num_kv_heads * p.n_new;
-  const int rows_total = 2 * rows_per_tensor;
-  for (int r = tid / R; r < rows_total; r += ROWS_PER_PASS) {
-    const int which = r / rows_per_tensor;  // 0 = K, 1 = V
+  for (int r = r0; r < rows_total; r += ROWS_PER_PASS) {
+    const int which = r / rows_per_tensor;
     const int rr = r - which * rows_per_tensor;
     const int h = rr / p.n_new;
     const int j = rr - h * p.n_new;
-    const uint16_t* src;
-    if (which == 0) {
-      src = static_cast<const uint16_t*>(p.k_src) + b * p.k_src_stride_b + h * p.k_src_stride_h +
-            j * p.k_src_stride_t;
-    } else {
-      src = static_cast<const uint16_t*>(p.v_src) + b * p.v_src_stride_b + h * p.v_src_stride_h +
-            j * p.v_src_stride_t;
-    }
-    const uint4 x = *reinterpret_cast<const uint4*>(src + lane * VEC);
+    const uint4 x = (r == r0) ? x_first : *reinterpret_cast<const uint4*>(src_row(r) + lane * VEC);
     int64_t row = 0, srow = 0;
     const bool ok = append_row_offset(p.cache, b, h, pos + j, row, srow, p.status);
     if constexpr (KV_DT == kFP8E4M3) {

@@ -37,6 +37,17 @@ def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+def _require_gpu(*tensors: torch.Tensor | None) -> None:
+    """Every tensor handed to a kernel must live on one GPU: a host pointer would be dereferenced on the
+    device. Raised here, before the library is called."""
+    devs = {t.device for t in tensors if t is not None}
+    for d in devs:
+        if d.type != "cuda":
+            raise AicasError(_lib.ERR_INVALID, f"tensors must be on a GPU (got {d})")
+    if len(devs) > 1:
+        raise AicasError(_lib.ERR_INVALID, f"tensors must be on one device (got {sorted(map(str, devs))})")
+
+
 def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
@@ -111,6 +122,7 @@ class KVCacheView:
         return self.k.device
 
     def desc(self) -> KVCacheDesc:
+        _require_gpu(self.k, self.v, self.k_scale, self.v_scale, self.block_table)
         d = KVCacheDesc()
         d.k = self.k.data_ptr()
         d.v = self.v.data_ptr()
@@ -164,9 +176,7 @@ def kv_append(
         raise AicasError(_lib.ERR_INVALID, "positions must be a contiguous int32 tensor with one entry per sequence")
     if seq_lens_out is not None and (seq_lens_out.dtype != torch.int32 or not seq_lens_out.is_contiguous()):
         raise AicasError(_lib.ERR_INVALID, "seq_lens_out must be a contiguous int32 tensor")
-    for t in (k_new, v_new, positions, seq_lens_out, status):
-        if t is not None and t.device != cache.device:
-            raise AicasError(_lib.ERR_INVALID, "all tensors must be on the cache's device")
+    _require_gpu(cache.k, k_new, v_new, positions, seq_lens_out, status)
     desc = cache.desc()
     check(
         _lib.lib().aicas_kv_append(
@@ -272,10 +282,7 @@ def decode_attention(
     if seq_lens is not None:
         if seq_lens.dtype != torch.int32 or seq_lens.numel() < B or not seq_lens.is_contiguous():
             raise AicasError(_lib.ERR_INVALID, "seq_lens must be a contiguous int32 tensor with one entry per sequence")
-        if seq_lens.device != cache.device:
-            raise AicasError(_lib.ERR_INVALID, "seq_lens must be on the cache's device")
-    if q4.device != cache.device:
-        raise AicasError(_lib.ERR_INVALID, "q must be on the cache's device")
+    _require_gpu(cache.k, q4, seq_lens, out, workspace, status)
     if out is None:
         out = torch.empty((B, Hq, 1, D), dtype=q.dtype, device=q.device)
     out4 = out.unsqueeze(2) if out.dim() == 3 else out
@@ -337,9 +344,7 @@ def decode_attention_append(
         raise AicasError(_lib.ERR_INVALID, "positions must be a contiguous int32 tensor with one entry per sequence")
     if seq_lens_out is not None and (seq_lens_out.dtype != torch.int32 or not seq_lens_out.is_contiguous()):
         raise AicasError(_lib.ERR_INVALID, "seq_lens_out must be a contiguous int32 tensor")
-    for t in (q4, kn, vn, positions, seq_lens_out, status):
-        if t is not None and t.device != cache.device:
-            raise AicasError(_lib.ERR_INVALID, "all tensors must be on the cache's device")
+    _require_gpu(cache.k, q4, kn, vn, positions, seq_lens_out, out, workspace, status)
     if out is None:
         out = torch.empty((B, Hq, 1, D), dtype=q.dtype, device=q.device)
     out4 = out.unsqueeze(2) if out.dim() == 3 else out

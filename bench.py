@@ -119,10 +119,14 @@ def main(argv=None) -> int:
     kn_all = normal((n_graph_steps, NL, B, HKV, 1, D), g, dev, scale=w.k_scale)
     vn_all = normal((n_graph_steps, NL, B, HKV, 1, D), g, dev)
     out_all = torch.zeros((n_graph_steps, NL, B, HQ, 1, D), dtype=torch.bfloat16, device=dev)
+    # fused path: one length tensor for the whole step (tokens cached before it), bumped by the last layer's
+    # kernel, as a serving loop keeps it; separate path: each layer's append bumps that layer's lengths
+    shared_lens = torch.full((B,), L0, dtype=torch.int32, device=dev)
     lens = [torch.full((B,), L0, dtype=torch.int32, device=dev) for _ in range(NL)]
     lens0 = torch.full((B,), L0, dtype=torch.int32, device=dev)
     views = [ops.KVCacheView(kbuf[i], vbuf[i]) for i in range(NL)]
-    plan = ops.decode_plan(torch.bfloat16, B, HQ, HKV, D, cap, 0, args.tokens_per_split)
+    # one split size for the whole run, planned at the longest step (the plan's workspace covers every step)
+    plan = ops.decode_plan(torch.bfloat16, B, HQ, HKV, D, L0 + n_graph_steps, 0, args.tokens_per_split)
     ws = ops.Workspace.reserve(dev, plan.workspace_bytes)
 
     def step(s, path, kernel_events=None):
@@ -132,8 +136,9 @@ def main(argv=None) -> int:
                 if kernel_events is not None:
                     kernel_events[i][0].record()
                 ops.decode_attention_append(
-                    q_all[s, i], views[i], kn_all[s, i], vn_all[s, i], lens[i], sm_scale=SM_SCALE, max_seq_len=cap,
-                    min_seq_len=L0 + s, seq_lens_out=lens[i], out=out_all[s, i],
+                    q_all[s, i], views[i], kn_all[s, i], vn_all[s, i], shared_lens, sm_scale=SM_SCALE,
+                    max_seq_len=L0 + s + 1, min_seq_len=L0 + s,
+                    seq_lens_out=shared_lens if i == NL - 1 else None, out=out_all[s, i],
                     tokens_per_split=plan.tokens_per_split, workspace=ws,
                 )
                 if kernel_events is not None:
@@ -143,13 +148,14 @@ def main(argv=None) -> int:
                 if kernel_events is not None:
                     kernel_events[i][0].record()
                 ops.decode_attention(
-                    q_all[s, i], views[i], sm_scale=SM_SCALE, seq_lens=lens[i], max_seq_len=cap,
+                    q_all[s, i], views[i], sm_scale=SM_SCALE, seq_lens=lens[i], max_seq_len=L0 + s + 1,
                     min_seq_len=L0 + s + 1, out=out_all[s, i], tokens_per_split=plan.tokens_per_split, workspace=ws,
                 )
                 if kernel_events is not None:
                     kernel_events[i][1].record()
 
     def reset_lens():
+        shared_lens.copy_(lens0)
         for t in lens:
             t.copy_(lens0)
 
