@@ -50,6 +50,8 @@ def parse_args(argv=None):
                    help="approximate CPU time budget for the oracle baseline (0 disables it)")
     p.add_argument("--kernel-timing-steps", type=int, default=8,
                    help="steps whose decode launches are bracketed by HIP events for the roofline")
+    p.add_argument("--copy-calibration-mib", type=int, default=0,
+                   help="also run a plain device copy of this many MiB (reference for profiler byte counters)")
     p.add_argument("--check-steps", type=int, default=2,
                    help="steps whose outputs are compared with the CPU oracle after timing")
     return p.parse_args(argv)
@@ -218,28 +220,44 @@ def main(argv=None) -> int:
     bytes_per_step = sum(bytes_steps) / K
     gbps = bytes_per_step / (us_per_step * 1e-6) / 1e9
 
-    # ---- decode-kernel duration: HIP events bracketing each decode launch, queued behind a GPU sleep so
-    # the host is ahead of the device and the events time the kernels, not Python
+    # ---- the dominant kernel's average duration. On the fused path every launch of the timed region is that
+    # kernel (NL per step, back to back in the replayed graphs), so the HIP-event time of the timed region over
+    # the number of launches is its average launch duration (launch gaps included). The separate path's
+    # decode launches are bracketed by events instead (queued behind a GPU sleep, so the host is ahead).
     kt_steps = min(args.kernel_timing_steps, K)
     durations = []
-    with torch.cuda.stream(stream):
-        reset_lens()
-        torch.cuda.synchronize()
-        evs = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(NL)] for _ in range(kt_steps)]
-        torch.cuda._sleep(int(1.0e8))
-        for s in range(kt_steps):
-            step(s, path, kernel_events=evs[s])
-        torch.cuda.synchronize()
-        for s in range(kt_steps):
-            for i in range(NL):
-                durations.append(evs[s][i][0].elapsed_time(evs[s][i][1]) * 1e3)  # us
-    dec_us = sum(durations) / len(durations)
+    if kt_steps > 0:
+        with torch.cuda.stream(stream):
+            reset_lens()
+            torch.cuda.synchronize()
+            evs = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(NL)]
+                   for _ in range(kt_steps)]
+            torch.cuda._sleep(int(1.0e8))
+            for s in range(kt_steps):
+                step(s, path, kernel_events=evs[s])
+            torch.cuda.synchronize()
+            for s in range(kt_steps):
+                for i in range(NL):
+                    durations.append(evs[s][i][0].elapsed_time(evs[s][i][1]) * 1e3)  # us
     if path == "fused":
-        # the fused kernel moves every algorithmic byte of the layer-step
-        dec_bytes = sum(algorithmic_bytes(B, HQ, HKV, D, lens_per_step[s]) for s in range(kt_steps)) / kt_steps
+        dec_us = us_per_step / NL
+        dec_bytes = bytes_per_step / NL  # the fused kernel moves every algorithmic byte of the layer-step
+        dec_launches = K * NL
     else:
+        dec_us = sum(durations) / len(durations)
         dec_bytes = sum(decode_kernel_bytes(B, HQ, HKV, D, lens_per_step[s]) for s in range(kt_steps)) / kt_steps
+        dec_launches = len(durations)
     dec_gbps = dec_bytes / (dec_us * 1e-6) / 1e9
+
+    # ---- a plain device copy of known size, for scaling the FETCH_SIZE / WRITE_SIZE counters of a profile run
+    if args.copy_calibration_mib > 0:
+        n = args.copy_calibration_mib << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).random_(0, 255)
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     # ---- parity of the timed run's first steps against the oracle (outputs of the timed replay)
     from oracle import reference_path as ref
@@ -295,6 +313,13 @@ def main(argv=None) -> int:
             "tokens_per_s": round(B / (cpu_us * 1e-6), 1),
         }
 
+    # HBM traffic per launch of the fused kernel, from the copy-calibrated FETCH_SIZE / WRITE_SIZE profile runs
+    traffic = None
+    traffic_file = os.path.join(ROOT, "profiles", "decode_append_c2_hbm_traffic.json")
+    if path == "fused" and os.path.exists(traffic_file):
+        with open(traffic_file) as f:
+            traffic = json.load(f)
+
     result = {
         "metric": "us/decode-step & achieved HBM GB/s (% of 8 TB/s), B=8 L=2048 28 layers",
         "value": round(us_per_step, 2),
@@ -329,10 +354,16 @@ def main(argv=None) -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(dec_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": None if traffic is None else traffic["traffic_bytes_per_launch"],
+            "traffic_note": None if traffic is None else (
+                f"rocprofv3 FETCH_SIZE x{traffic['fetch_scale']} + WRITE_SIZE x{traffic['write_scale']} "
+                f"(scales from a 256 MiB copy), {traffic['profiled_lengths']}; "
+                f"{traffic['traffic_over_algorithmic']} of the algorithmic bytes at those lengths "
+                "(profiles/decode_append_c2_hbm_traffic.md)"),
             "avg_launch_us": round(dec_us, 3),
+            "avg_launch_us_event_bracketed": round(sum(durations) / len(durations), 3) if durations else None,
             "bytes_per_launch": int(dec_bytes),
-            "launches_timed": len(durations),
+            "launches_timed": dec_launches,
         },
         "cpu_baseline": cpu,
         "parity_max_abs_err": max_err,
