@@ -18,7 +18,7 @@ import torch  # noqa: F401  (must precede the library load, see above)
 LIB_NAME = "libaicas_decode.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_BF16 = 0
 DTYPE_FP16 = 1

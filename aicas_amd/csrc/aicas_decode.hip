@@ -159,10 +159,19 @@ int launch_decode(const aicas::DecodeParams& p, int q_dtype, int kv_dtype, int d
 // 28-layer B=8 L=2048 decode (4 to 12 splits per (batch, kv head) pair within 7% of each other).
 constexpr int kWorkgroupsPerCUx4 = 7;
 
+// Workspace layout. The counters sit at fixed offsets, the same for every launch shape, ahead of the
+// partials: they are zero between launches whatever shapes ran before on the same workspace, since no launch
+// ever stores partials there. A launch may cover at most kMaxPairs (batch row, kv head) pairs.
+constexpr int64_t kMaxPairs = 65536;
+constexpr size_t kCounterBytes = kMaxPairs * sizeof(int32_t);
+constexpr size_t kArrivalOff = 0;                  // [pairs] split arrivals
+constexpr size_t kBatchArriveOff = kCounterBytes;  // [batch] readers of positions[b]
+constexpr size_t kPartialsOff = 2 * kCounterBytes;
+
 struct Plan {
   int32_t tokens_per_split;
   int32_t num_splits;
-  size_t counter_off, arrive_off, ml_off, acc_off, bytes;
+  size_t ml_off, acc_off, bytes;
 };
 
 int plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
@@ -171,6 +180,9 @@ int plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int32_t num_kv_he
   if (!valid_head_dim(head_dim)) return fail(AICAS_ERR_UNSUPPORTED, "head_dim %d not supported", head_dim);
   if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_seq_len < 0)
     return fail(AICAS_ERR_INVALID, "batch/heads must be positive and max_seq_len non-negative");
+  if (int64_t{batch} * num_kv_heads > kMaxPairs)
+    return fail(AICAS_ERR_UNSUPPORTED, "batch * num_kv_heads = %lld exceeds %lld", (long long)batch * num_kv_heads,
+                (long long)kMaxPairs);
   const int tpi = tokens_per_iteration(kv_dtype, head_dim);
   const int rpb = rows_per_load(kv_dtype, head_dim);
   int64_t tps;
@@ -185,9 +197,9 @@ int plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int32_t num_kv_he
     tps = ceil_div(tps, rpb) * rpb;
     if (tps < tpi) tps = tpi;
   }
-  // A split may touch at most kMaxBlockEntries block-table entries.
+  // A split streaming a static range may touch at most kMaxBlockEntries block-table entries.
   if (page_size > 0) {
-    const int64_t cap = (int64_t{aicas::kMaxBlockEntries} - 1) * page_size / tpi * tpi;
+    const int64_t cap = (int64_t{aicas::kMaxBlockEntries} - 2) * page_size / tpi * tpi;
     if (cap >= tpi && tps > cap) tps = cap;
   }
   if (tps > (int64_t{1} << 30)) tps = int64_t{1} << 30;
@@ -196,9 +208,7 @@ int plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int32_t num_kv_he
   pl.tokens_per_split = static_cast<int32_t>(tps);
   pl.num_splits = static_cast<int32_t>(splits);
   const size_t parts = size_t(batch) * num_q_heads * splits;
-  pl.counter_off = 0;
-  pl.arrive_off = align_up(size_t(batch) * num_kv_heads * sizeof(int32_t), 256);
-  pl.ml_off = pl.arrive_off + align_up(size_t(batch) * sizeof(int32_t), 256);
+  pl.ml_off = kPartialsOff;
   pl.acc_off = pl.ml_off + align_up(parts * 2 * sizeof(float), 256);
   pl.bytes = pl.acc_off + align_up(parts * head_dim * sizeof(float), 256);
   return AICAS_OK;
@@ -267,8 +277,8 @@ int run_decode(const DecodeCall& c, hipStream_t stream) {
   p.max_splits = pl.num_splits;
   p.page_shift = c.cache->block_table ? ilog2(c.cache->page_size) : 0;
   p.scale_log2 = c.sm_scale * 1.4426950408889634f;
-  p.ws_counter = reinterpret_cast<int32_t*>(ws + pl.counter_off);
-  p.ws_arrive = reinterpret_cast<int32_t*>(ws + pl.arrive_off);
+  p.ws_counter = reinterpret_cast<int32_t*>(ws + kArrivalOff);
+  p.ws_arrive = reinterpret_cast<int32_t*>(ws + kBatchArriveOff);
   p.ws_ml = reinterpret_cast<float*>(ws + pl.ml_off);
   p.ws_acc = reinterpret_cast<float*>(ws + pl.acc_off);
   p.status = c.status;

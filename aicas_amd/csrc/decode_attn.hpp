@@ -5,11 +5,18 @@
 // which is what the reference decode path returns (triton_qwen3vl/gqa_decode_attention.py:46-141 and its
 // oracle, SDPA over repeat_kv, triton_qwen3vl/fallback.py:7-64), with per-sequence lengths L_b.
 //
-// Work decomposition: one 256-thread workgroup per (split, kv head, batch row); a split is a range of
-// tokens_per_split tokens. Every K/V row is read once and serves all G query heads of the group. A row of D
-// elements is spread over R = D / VEC lanes (16 bytes per lane), so one wave load instruction covers 64 / R
-// consecutive tokens (1 KiB). Loads are double-buffered in registers: the next chunk of U tokens per lane is
-// in flight while the current one is consumed, which keeps ~16 KiB per wave outstanding.
+// Work decomposition: one 256-thread workgroup per (split, kv head, batch row); a sequence of L tokens gets
+// n = ceil(L / tokens_per_split) active workgroups. Every K/V row is read once and serves all G query heads of
+// the group. A row of D elements is spread over R = D / VEC lanes (16 bytes per lane), so one wave load
+// instruction covers 64 / R consecutive tokens (1 KiB). Each wave streams its own super-chunks of 2 x U such
+// loads (16 KiB of K and V), double-buffered in registers: one chunk of U loads is in flight while the other
+// is consumed.
+//
+// Scheduling (striped mode): the super-chunks of a sequence are dealt round-robin to the 4 * n waves of its
+// workgroups (wave slot w takes super-chunks w, w + 4n, w + 8n, ...), so that every wave carries the same work
+// to one super-chunk and the waves of the sequence sweep its K/V together. Paged caches whose block-table
+// row does not fit the LDS cache use range mode: each split streams a static range of equal size (to a load
+// group), its 4 waves taking super-chunks of it in turn.
 //
 // Each R-lane row group keeps its own online-softmax state (running max m, sum l, accumulator acc) in fp32
 // in the exp2 domain; the states are merged across the row groups of a wave with lane shuffles and across the
@@ -19,15 +26,16 @@
 // write through to the device coherence point, so no L2 writeback is needed), waits for them to complete,
 // and bumps the (b, kv head) arrival counter. The split that arrives last reads every split's partial with
 // agent-scope loads and combines them: M = max m_i, l = sum l_i 2^(m_i - M), out = sum acc_i 2^(m_i - M) / l;
-// it then re-arms the counter to zero. Nothing ever waits on another workgroup. Sequences that need one split
-// write the output directly.
+// it then re-arms the counter to zero. Nothing ever waits on another workgroup. Sequences that need one
+// split write the output directly.
 //
-// Prologue: q and, for contiguous caches whose lengths the caller bounds from below (spec_len), the first
-// chunk of K/V are fetched before the lengths are read, so that their latencies overlap.
+// Prologue: q, the new rows (APPEND) and, for contiguous caches whose lengths the caller bounds from below
+// (spec_len), the first chunk of each wave's static super-chunk are fetched before the lengths are read, so
+// that their latencies overlap.
 //
 // Fused append (APPEND): positions[b] is the length before this step; the kernel attends over
 // L_b = positions[b] + 1 tokens, takes token L_b - 1 from the new rows (k_new / v_new) instead of the cache,
-// and the workgroup that owns that token writes the row into the cache (quantized on write for fp8 caches,
+// and split 0 writes the row into the cache (quantized on write for fp8 caches,
 // with the attention then using the dequantised row, exactly what a separate append followed by attention
 // would read). Every workgroup of batch row b counts itself in when it exits (it read positions[b] at the
 // start); the last one to do so stores positions[b] + 1 to seq_lens_out[b] (which may alias positions), so
@@ -65,7 +73,7 @@ struct DecodeParams {
   int32_t spec_len;  // caller-guaranteed lower bound on every sequence's cached length (0: none)
 };
 
-constexpr int kMaxBlockEntries = 1024;  // block-table entries one split may touch (LDS cache)
+constexpr int kMaxBlockEntries = 2048;  // block-table entries a workgroup can hold in LDS
 constexpr float kNegBig = -1.0e30f;     // finite "minus infinity" for running maxima
 
 template <int KV_DT>
@@ -129,7 +137,7 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   const int kvh = blockIdx.y;
   const int b = blockIdx.z;
   const int tid = threadIdx.x;
-  const int wave = tid / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // uniform across the wave: scalar control flow
   const int lane = tid % kWave;
   const int row = lane / R;
   const int li = lane % R;
@@ -165,33 +173,70 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   const int64_t shead_off = static_cast<int64_t>(kvh) * p.cache.scale_stride_h;
   const int page_mask = (1 << p.page_shift) - 1;
   const int tps = p.tokens_per_split;
-  const int t_begin = split * tps;
   // Clamp so that no access leaves the cache or the launched split range.
   const int limit = min(p.cache.max_tokens, tps * p.max_splits);
+  // A wave streams chunks of CW consecutive tokens (U loads of RPW rows); its unit of work is a super-chunk of
+  // two chunks, one per register buffer. Super-chunk j covers tokens [j * SCW, (j + 1) * SCW).
+  constexpr int CW = U * RPW;
+  constexpr int SCW = 2 * CW;
+  const int wave_slot = split * kWavesPerBlock + wave;  // this wave's first super-chunk in striped mode
+  // Range mode: the n splits of an L-token sequence cover [begin(s), begin(s + 1)), whole groups of RPB tokens
+  // each, so that their sizes differ by at most one group and none exceeds tps rounded up to a group.
+  auto split_begin = [](int s, int n, int len) {
+    const int64_t groups = (len + RPB - 1) / RPB;
+    return min(len, static_cast<int>(static_cast<int64_t>(s) * groups / n) * RPB);
+  };
 
-  // Contiguous caches whose every sequence is known (spec_len, from the caller) to hold the first chunk of this
-  // split: fetch that chunk now, so that it overlaps the read of the lengths.
-  Chunk<KV_DT, U> ca, cb;
-  const bool spec = !PAGED && t_begin + TPI <= p.spec_len && t_begin + TPI <= limit;
-  if (spec) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int t = t_begin + u * RPB + wave * RPW + row;
-      const int64_t off = static_cast<int64_t>(b) * p.cache.stride_blk + head_off +
-                          static_cast<int64_t>(t) * p.cache.stride_t;
-      ca.k[u] = *reinterpret_cast<const uint4*>(kbase + off * EB + li * 16);
-      ca.v[u] = *reinterpret_cast<const uint4*>(vbase + off * EB + li * 16);
-      if constexpr (FP8) {
-        const int64_t soff = static_cast<int64_t>(b) * p.cache.scale_stride_blk + shead_off + t;
-        ca.ks[u] = p.cache.k_scale[soff];
-        ca.vs[u] = p.cache.v_scale[soff];
-      } else {
-        ca.ks[u] = 0.0f;
-        ca.vs[u] = 0.0f;
-      }
-      ca.ok[u] = true;
+  // APPEND: the new token's source rows (lanes tid < 2R; K then V), fetched now: they do not depend on the
+  // lengths.
+  uint4 new_raw[FP8 ? 2 : 1];
+  if constexpr (APPEND) {
+    if (tid < 2 * R) {
+      const int c = tid % R;
+      const uint16_t* src = tid < R
+          ? static_cast<const uint16_t*>(p.k_new) + b * p.kn_stride_b + kvh * p.kn_stride_h
+          : static_cast<const uint16_t*>(p.v_new) + b * p.vn_stride_b + kvh * p.vn_stride_h;
+      new_raw[0] = *reinterpret_cast<const uint4*>(src + c * VEC);
+      if constexpr (FP8) new_raw[1] = *reinterpret_cast<const uint4*>(src + c * VEC + 8);
     }
   }
+
+  // Issues the loads of rows t0 + u * RPW + row of this wave (hi >= 1). Rows at or past hi, the row `skip`
+  // and rows on invalid pages come out with ok = false; they still load, from row min(t, hi - 1) (block 0 for
+  // an invalid page), so that every load is issued on every path and the compiler can wait for one buffer
+  // while the other stays in flight. Their words are never let through by consume.
+  auto load_rows = [&](Chunk<KV_DT, U>& c, int t0, int hi, int skip, int first_entry) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int t = t0 + u * RPW + row;
+      const int tc = min(t, hi - 1);
+      bool ok = t < hi && t != skip;
+      int64_t blk = b;
+      int tin = tc;
+      if constexpr (PAGED) {
+        const int32_t e = s_bt[(tc >> p.page_shift) - first_entry];
+        ok = ok && e >= 0;
+        blk = e >= 0 ? e : 0;
+        tin = tc & page_mask;
+      }
+      const int64_t off = blk * p.cache.stride_blk + head_off + static_cast<int64_t>(tin) * p.cache.stride_t;
+      c.k[u] = *reinterpret_cast<const uint4*>(kbase + off * EB + li * 16);
+      c.v[u] = *reinterpret_cast<const uint4*>(vbase + off * EB + li * 16);
+      if constexpr (FP8) {
+        const int64_t soff = blk * p.cache.scale_stride_blk + shead_off + tin;
+        c.ks[u] = p.cache.k_scale[soff];
+        c.vs[u] = p.cache.v_scale[soff];
+      }
+      c.ok[u] = ok;
+    }
+  };
+
+  // Contiguous caches whose every sequence is known (spec_len, from the caller) to hold at least spec_len
+  // tokens: the first chunk of this wave's static super-chunk is fetched before the lengths are read, so that
+  // the two latencies overlap.
+  Chunk<KV_DT, U> ca, cb;
+  const bool spec_issued = !PAGED && p.spec_len > 0 && wave_slot * SCW + CW <= min(p.spec_len, limit);
+  if (spec_issued) load_rows(ca, wave_slot * SCW, limit, -1, 0);
 
   // Sequence length (cached tokens before this step's append for APPEND).
   if (tid == 0) s_len = p.seq_lens ? p.seq_lens[b] : p.uniform_len;
@@ -234,9 +279,21 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
     count_in();
     return;
   }
-  const int t_end = min(t_begin + tps, L);
 
-  // Paged caches: stage this split's block ids in LDS (invalid ids become -1 and their tokens are skipped).
+  // Schedule: striped mode unless a paged sequence's whole block-table row does not fit the LDS cache.
+  bool striped = true;
+  if constexpr (PAGED) striped = ((L + page_mask) >> p.page_shift) <= kMaxBlockEntries;
+  const int n_super = (L + SCW - 1) / SCW;
+  const int stripe = n_active * kWavesPerBlock;  // striped mode: waves sharing the sequence
+  const int t_begin = striped ? 0 : split_begin(split, n_active, L);
+  const int t_end = striped ? L : split_begin(split + 1, n_active, L);
+  // The speculative chunk is this wave's first unit of work (striped mode, the only mode of contiguous
+  // caches); if a length falls short of spec_len after all, its rows at or past L (and the new token's row)
+  // are masked below instead of being read again.
+  const bool spec = spec_issued;
+
+  // Paged caches: stage the block ids this workgroup may touch in LDS (invalid ids become -1 and their tokens
+  // are skipped): the whole row in striped mode, the split's range otherwise.
   int first_entry = 0;
   if constexpr (PAGED) {
     first_entry = t_begin >> p.page_shift;
@@ -251,34 +308,31 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
       s_bt[i] = blk;
     }
   }
-  // APPEND: the workgroup owning the new token writes its rows into the cache and stages them in LDS.
+  // APPEND: every workgroup stages the new token's rows in LDS as the attention must see them (whichever wave
+  // streams token t_new takes it from there); split 0 also writes them into the cache. For fp8 caches the rows
+  // are quantized on write exactly as aicas_kv_append does, and the attention uses the dequantised codes.
   if constexpr (APPEND) {
-    if (t_new >= t_begin && t_new < t_end && tid < 2 * R) {
+    if (t_new >= 0 && tid < 2 * R) {
       const int which = tid / R;  // 0 = K, 1 = V
       const int c = tid % R;
-      const uint16_t* src = which == 0
-          ? static_cast<const uint16_t*>(p.k_new) + b * p.kn_stride_b + kvh * p.kn_stride_h
-          : static_cast<const uint16_t*>(p.v_new) + b * p.vn_stride_b + kvh * p.vn_stride_h;
       int64_t blk = b;
       int tin = t_new;
-      bool ok = true;
+      bool ok = split == 0;
       if constexpr (PAGED) {
         blk = p.cache.block_table[static_cast<int64_t>(b) * p.cache.block_table_stride + (t_new >> p.page_shift)];
         tin = t_new & page_mask;
-        ok = blk >= 0 && blk < p.cache.num_blocks;
+        ok = ok && blk >= 0 && blk < p.cache.num_blocks;
       }
       const int64_t off = blk * p.cache.stride_blk + head_off + static_cast<int64_t>(tin) * p.cache.stride_t;
       void* dst_base = which == 0 ? p.cache.k : p.cache.v;
       if constexpr (!FP8) {
-        const uint4 x = *reinterpret_cast<const uint4*>(src + c * VEC);
-        if (ok) *reinterpret_cast<uint4*>(static_cast<uint16_t*>(dst_base) + off + c * VEC) = x;
-        s_new[tid] = x;
+        if (ok) *reinterpret_cast<uint4*>(static_cast<uint16_t*>(dst_base) + off + c * VEC) = new_raw[0];
+        s_new[tid] = new_raw[0];
       } else {
         // VEC = 16 source elements (32 bytes) per lane -> 16 codes
         float f[VEC];
-        const uint4 x0 = *reinterpret_cast<const uint4*>(src + c * VEC);
-        const uint4 x1 = *reinterpret_cast<const uint4*>(src + c * VEC + 8);
-        const uint32_t w[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        const uint32_t w[8] = {new_raw[0].x, new_raw[0].y, new_raw[0].z, new_raw[0].w,
+                               new_raw[1].x, new_raw[1].y, new_raw[1].z, new_raw[1].w};
 #pragma unroll
         for (int i = 0; i < 8; ++i) unpack2<Q_DT>(w[i], f[2 * i], f[2 * i + 1]);
         float amax = 0.0f;
@@ -308,48 +362,39 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   }
   __syncthreads();
 
-  auto load_chunk = [&](Chunk<KV_DT, U>& c, int t0) {
+  // Token t_new of a chunk comes from the staged new rows (only the chunk holding it takes this branch).
+  auto take_new_row = [&](Chunk<KV_DT, U>& c, int t0) {
+    if constexpr (APPEND) {
+      if (t_new >= t0 && t_new < t0 + CW) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int t = t0 + u * RPB + wave * RPW + row;
-      bool ok = t < t_end;
-      c.k[u] = make_uint4(0u, 0u, 0u, 0u);
-      c.v[u] = make_uint4(0u, 0u, 0u, 0u);
-      c.ks[u] = 0.0f;
-      c.vs[u] = 0.0f;
-      // only the split that owns the new token (t < t_end) staged its rows in LDS
-      if (APPEND && ok && t == t_new) {
-        c.k[u] = s_new[li];
-        c.v[u] = s_new[R + li];
-        if constexpr (FP8) {
-          c.ks[u] = s_new_scale[0];
-          c.vs[u] = s_new_scale[1];
-        }
-        c.ok[u] = true;
-        continue;
-      }
-      int64_t blk = b;
-      int tin = t;
-      if constexpr (PAGED) {
-        if (ok) {
-          blk = s_bt[(t >> p.page_shift) - first_entry];
-          tin = t & page_mask;
-          ok = blk >= 0;
+        for (int u = 0; u < U; ++u) {
+          if (t0 + u * RPW + row == t_new) {
+            c.k[u] = s_new[li];
+            c.v[u] = s_new[R + li];
+            if constexpr (FP8) {
+              c.ks[u] = s_new_scale[0];
+              c.vs[u] = s_new_scale[1];
+            }
+            c.ok[u] = true;
+          }
         }
       }
-      if (ok) {
-        const int64_t off = blk * p.cache.stride_blk + head_off + static_cast<int64_t>(tin) * p.cache.stride_t;
-        c.k[u] = *reinterpret_cast<const uint4*>(kbase + off * EB + li * 16);
-        c.v[u] = *reinterpret_cast<const uint4*>(vbase + off * EB + li * 16);
-        if constexpr (FP8) {
-          const int64_t soff = blk * p.cache.scale_stride_blk + shead_off + tin;
-          c.ks[u] = p.cache.k_scale[soff];
-          c.vs[u] = p.cache.v_scale[soff];
-        }
-      }
-      c.ok[u] = ok;
     }
   };
+  // One chunk of rows: from the cache, or (token t_new) from the staged new rows.
+  auto load_chunk = [&](Chunk<KV_DT, U>& c, int t0) {
+    load_rows(c, t0, t_end, t_new, first_entry);
+    take_new_row(c, t0);
+  };
+  if (spec) {
+    const int t0 = wave_slot * SCW;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int t = t0 + u * RPW + row;
+      ca.ok[u] = ca.ok[u] && t < L && t != t_new;
+    }
+    take_new_row(ca, t0);
+  }
 
   float m[G], l[G], acc[G][VEC];
 #pragma unroll
@@ -415,7 +460,9 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       float vf[VEC];
-      const uint32_t vw[4] = {c.v[u].x, c.v[u].y, c.v[u].z, c.v[u].w};
+      // a masked row's weight is 0, but its registers hold stale words that must not reach the FMA as NaN/Inf
+      const uint32_t vw[4] = {c.ok[u] ? c.v[u].x : 0u, c.ok[u] ? c.v[u].y : 0u, c.ok[u] ? c.v[u].z : 0u,
+                              c.ok[u] ? c.v[u].w : 0u};
       if constexpr (!FP8) {
 #pragma unroll
         for (int w = 0; w < 4; ++w) unpack2<KV_DT>(vw[w], vf[2 * w], vf[2 * w + 1]);
@@ -434,26 +481,57 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
       for (int h = 0; h < G; ++h) {
         const float pu = fast_exp2(s[u][h] - mnew[h]);
         l[h] += pu;
-        const float pv = FP8 ? pu * c.vs[u] : pu;
+        const float pv = FP8 ? (c.ok[u] ? pu * c.vs[u] : 0.0f) : pu;
 #pragma unroll
         for (int i = 0; i < VEC; ++i) acc[h][i] = fmaf(pv, vf[i], acc[h][i]);
       }
     }
   };
 
-  // Double-buffered token loop: chunk j+1 is in flight while chunk j is consumed.
+  // Token loop over super-chunks, double-buffered: chunk 1 of a super-chunk is in flight while chunk 0 is
+  // consumed, and chunk 0 of the next super-chunk while chunk 1 is.
   {
-    int t0 = t_begin;
-    if (!spec && t0 < t_end) load_chunk(ca, t0);
-    while (t0 < t_end) {
-      const int t1 = t0 + TPI;
-      if (t1 < t_end) load_chunk(cb, t1);
+    int k = 0;  // super-chunks of this wave taken so far
+    auto super_start = [&](int i) -> int {
+      if (striped) {
+        const int j = wave_slot + i * stripe;
+        return j < n_super ? j * SCW : -1;
+      }
+      const int t = t_begin + (wave + i * kWavesPerBlock) * SCW;
+      return t < t_end ? t : -1;
+    };
+    const int sc = super_start(0);
+    if (sc >= 0) {
+      if (!spec) load_chunk(ca, sc);
+      load_chunk(cb, sc + CW);
+      // settle() pins the softmax state after a consume: the empty asm statements take every state register as
+      // an operand and the last one orders memory, so the whole consume (its last use of the buffer) precedes
+      // the reload that follows, and the new rows land in the registers of the old ones. Without it the
+      // compiler sinks the P.V half of a consume past the next loads and copies the buffers on every round,
+      // each copy waiting for its load. The scheduling barrier after each reload keeps its loads from sinking
+      // into the consume that follows. The last super-chunk is consumed after the loop, so that no load is
+      // issued past the end.
+      auto settle = [&]() {
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+          asm volatile("" : "+v"(m[h]), "+v"(l[h]));
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) asm volatile("" : "+v"(acc[h][i]));
+        }
+        asm volatile("" ::: "memory");
+      };
+      for (int nsc = super_start(++k); nsc >= 0; nsc = super_start(++k)) {
+        consume(ca);
+        settle();
+        load_chunk(ca, nsc);
+        __builtin_amdgcn_sched_barrier(0);
+        consume(cb);
+        settle();
+        load_chunk(cb, nsc + CW);
+        __builtin_amdgcn_sched_barrier(0);
+      }
       consume(ca);
-      if (t1 >= t_end) break;
-      const int t2 = t1 + TPI;
-      if (t2 < t_end) load_chunk(ca, t2);
       consume(cb);
-      t0 = t2;
     }
   }
 

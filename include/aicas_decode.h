@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define AICAS_ABI_VERSION 2
+#define AICAS_ABI_VERSION 3
 
 /* Element types. */
 #define AICAS_DTYPE_BF16 0
@@ -102,8 +102,10 @@ int aicas_kv_append(const aicas_kv_cache_t* cache, int32_t src_dtype, const void
 /*
  * Launch plan for aicas_decode_attention: the token range per split (tokens_per_split_hint, or 0 to choose
  * automatically), the number of splits covering max_seq_len, and the workspace size in bytes. The
- * workspace must be zero-filled once when first allocated; the kernels leave it re-armed (zero arrival
- * counters) after every launch. Two launches that may run concurrently need two workspaces.
+ * workspace starts with 512 KiB of counters at fixed offsets, followed by the split partials; it must be
+ * zero-filled once when first allocated, and the kernels leave the counters at zero after every launch, so
+ * launches of any shapes may share one workspace in turn. Two launches that may run concurrently need two
+ * workspaces. batch * num_kv_heads may not exceed 65536.
  * Replaces: triton_qwen3vl/gqa_decode_attention.py:287-292 (block size / warps choice).
  */
 int aicas_decode_plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
@@ -118,8 +120,8 @@ int aicas_decode_plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int3
  * AICAS_STATUS_LEN_CLAMPED is set. An empty sequence (L_b == 0) yields zeros. head_dim in {16, 32, 64, 128},
  * G in {1, 2, 4, 8}. tokens_per_split as from aicas_decode_plan (0 = automatic). min_len is a lower bound on every
  * L_b that the caller guarantees (0 if unknown; ignored when seq_lens is NULL): it lets contiguous-cache
- * kernels start reading K/V before they have read seq_lens. A min_len above some L_b makes that sequence's
- * result undefined (never out of bounds).
+ * kernels start reading K/V before they have read seq_lens. A min_len above some L_b only costs that sequence
+ * the early start (reads stay inside the cache, the result is unchanged).
  * Replaces: triton_qwen3vl/gqa_decode_attention.py:46-141, :268-327; dujunbaoV1/native_cuda_ops/
  * decode_q1_gqa.cpp:73-95; new KV cache/evaluation_wrapper.py:248-265.
  */
