@@ -1,23 +1,33 @@
 """Decode-step benchmark: KV append + GQA decode attention, Qwen3-VL-2B text-decoder shapes, one MI355X.
 
-Default workload (the headline configuration): batch 8, 16 query / 8 kv heads, head_dim 128, bf16,
-28 layers, each sequence prefilled with 2048 tokens (N(0,1), K scaled by 0.5), then decode steps that each
-run, for every layer, one KV append (1 token per sequence) and one decode attention over the whole cache.
-A step is therefore 28 x {append, attend}; --steps K times exactly K steps (K=128 is one full 128-token
-generation), after --warmup W untimed steps. Cache lengths are reset to 2048 between warmup and timing.
+Default workload (the headline configuration, --config c2): batch 8, 16 query / 8 kv heads, head_dim 128,
+bf16, 28 layers, each sequence prefilled with 2048 tokens (N(0,1), K scaled by 0.5), then decode steps that
+each run, for every layer, one KV append (1 token per sequence) and one decode attention over the whole
+cache. A step is therefore 28 x {append, attend}; --steps K times exactly K steps (K=128 is one full
+128-token generation), after --warmup W untimed steps. Cache lengths are reset between warmup and timing.
 The default path runs each layer's append + attend as one launch (aicas_decode_attention_append); the
 two-launch path (aicas_kv_append, then aicas_decode_attention) is timed beside it and reported.
 
+The other seeded configurations of aicas_amd.workloads run with --config:
+  c1  B=1, 1 layer, 1024 cached, one step (append at 1024, attend over 1025), repeated;
+  c3  B=1, 1 layer, 32768 cached, 64 growing steps;
+  c4  B=64, 28 layers, ragged lengths ~ U{512..4096}, one step, repeated;
+  c5  B=32, 1 layer, ragged lengths ~ U{256..8192}, paged fp8 (16-token pages, permuted block table, 1%
+      outliers), one step, repeated.
+A one-layer configuration whose cache is smaller than 512 MB keeps several instances of it (>= 4, > 512 MB in
+all) and steps through them in turn, so that the 256 MB MALL cannot serve the reads; its step time is the
+per-layer time. One-step configurations repeat their step with the positions held, so every repeat appends
+at the same position and attends over the same lengths.
+
 Each decode step is captured once as a HIP graph (torch.cuda.CUDAGraph) over per-(step, layer) input and
 output buffers, as a serving loop replays one graph per generated token; the timed region is K back-to-back
-replays bracketed by torch.cuda.synchronize() and HIP events. --mode eager times the same work issued from
-Python without graphs (host-bound).
+replays bracketed by torch.cuda.synchronize() and HIP events (one event between replays gives the per-step
+median and p90). --mode eager times the same work issued from Python without graphs (host-bound).
 
 Printed JSON line: value = microseconds per decode step (lower is better), plus tokens/s, algorithmic HBM
-bytes per step and GB/s, the decode kernel's roofline (average duration of the decode kernel from HIP events
-bracketing each launch on its stream, algorithmic bytes per launch / that duration), and a CPU baseline: the
-oracle (torch.cat append + SDPA over repeat_kv, bf16 eager on the host cores) on the first steps of the same
-inputs.
+bytes per step and GB/s, the decode kernel's roofline (algorithmic bytes per launch / average launch
+duration on its stream), and a CPU baseline: the oracle (torch.cat append + SDPA over repeat_kv, bf16 eager
+on the host cores; for the paged fp8 configuration, dequantise + SDPA) on a bounded sample of the same steps.
 """
 
 from __future__ import annotations
@@ -34,12 +44,14 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
+MALL_BYTES = 256 << 20
 
 
 def parse_args(argv=None):
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=128)
+    p.add_argument("--config", choices=("c1", "c2", "c3", "c4", "c5"), default="c2")
+    p.add_argument("--steps", type=int, default=0, help="timed steps (0: the configuration's default)")
     p.add_argument("--warmup", type=int, default=16)
     p.add_argument("--mode", choices=("graph", "eager"), default="graph")
     p.add_argument("--path", choices=("fused", "separate"), default="fused",
@@ -49,7 +61,7 @@ def parse_args(argv=None):
     p.add_argument("--cpu-baseline-seconds", type=float, default=15.0,
                    help="approximate CPU time budget for the oracle baseline (0 disables it)")
     p.add_argument("--kernel-timing-steps", type=int, default=8,
-                   help="steps whose decode launches are bracketed by HIP events for the roofline")
+                   help="steps whose launches are bracketed by HIP events (two-launch path roofline)")
     p.add_argument("--copy-calibration-mib", type=int, default=0,
                    help="also run a plain device copy of this many MiB (reference for profiler byte counters)")
     p.add_argument("--check-steps", type=int, default=2,
@@ -57,18 +69,28 @@ def parse_args(argv=None):
     return p.parse_args(argv)
 
 
-def algorithmic_bytes(batch, hq, hkv, d, lens_after, elem=2):
+def kv_elem_bytes(fp8):
+    """Bytes per cached element and per (token, kv head) scale."""
+    return (1, 4) if fp8 else (2, 0)
+
+
+def algorithmic_bytes(batch, hq, hkv, d, lens_after, fp8=False, page=0):
     """Bytes one layer-step must move: K and V read over each sequence's cache (length after the append),
-    new K/V rows read and written, q read and the output written."""
-    kv_read = sum(2 * L * hkv * d * elem for L in lens_after)
-    new_rows = 2 * batch * hkv * d * 2 + 2 * batch * hkv * d * elem
+    new K/V rows read (bf16) and written (cache format), q read and the output written, and for paged caches
+    the block-table entries and lengths read."""
+    e, s = kv_elem_bytes(fp8)
+    kv_read = sum(2 * L * hkv * (d * e + s) for L in lens_after)
+    new_rows = 2 * batch * hkv * d * 2 + 2 * batch * hkv * (d * e + s)
     q_out = 2 * batch * hq * d * 2
-    return kv_read + new_rows + q_out
+    table = (sum((L + page - 1) // page * 4 for L in lens_after) + batch * 4) if page else 0
+    return kv_read + new_rows + q_out + table
 
 
-def decode_kernel_bytes(batch, hq, hkv, d, lens_after, elem=2):
-    """Bytes of the decode launch alone: K/V over the cache, q in, out out."""
-    return sum(2 * L * hkv * d * elem for L in lens_after) + 2 * batch * hq * d * 2
+def decode_kernel_bytes(batch, hq, hkv, d, lens_after, fp8=False, page=0):
+    """Bytes of the decode launch alone (two-launch path): K/V over the cache, q in, out out, table."""
+    e, s = kv_elem_bytes(fp8)
+    table = (sum((L + page - 1) // page * 4 for L in lens_after) + batch * 4) if page else 0
+    return sum(2 * L * hkv * (d * e + s) for L in lens_after) + 2 * batch * hq * d * 2 + table
 
 
 def cpu_info():
@@ -84,6 +106,15 @@ def cpu_info():
     return model
 
 
+def percentile(xs, p):
+    ys = sorted(xs)
+    if not ys:
+        return None
+    k = (len(ys) - 1) * p
+    lo, hi = math.floor(k), math.ceil(k)
+    return ys[lo] + (ys[hi] - ys[lo]) * (k - lo)
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
@@ -94,53 +125,86 @@ def main(argv=None) -> int:
     import torch
 
     from aicas_amd import ops
-    from aicas_amd.workloads import HEAD_DIM, HKV, HQ, SM_SCALE, WORKLOADS, generator, normal
+    from aicas_amd.workloads import HEAD_DIM, HKV, HQ, PAGE, SM_SCALE, WORKLOADS, generator, normal, seq_lengths
 
-    w = WORKLOADS["c2"]
+    w = WORKLOADS[args.config]
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    B, D, L0, NL = w.batch, HEAD_DIM, w.prefill, w.layers
-    K, W = args.steps, args.warmup
-    n_graph_steps = max(K, W)
-    cap = L0 + n_graph_steps
-    cap = (cap + 63) // 64 * 64
+    B, D = w.batch, HEAD_DIM
+    G = HQ // HKV
+    growing = w.steps > 1  # c2, c3: every step appends a new token; c1, c4, c5: one step, repeated
+    K = args.steps or (w.steps if growing else 64)
+    W = args.warmup
+    n_graph_steps = max(K, W) if growing else 1
+    gen = generator(dev, w.seed)
+    base = [w.prefill] * B if w.len_range is None else seq_lengths(w, gen)  # cached before step 0
+    page = PAGE if w.paged else 0
+    kv_dtype = ops.FP8_DTYPE if w.fp8 else torch.bfloat16
+    # cache instances: the configuration's layers, or for one-layer configurations enough copies to exceed
+    # twice the MALL (>= 4), stepped through in turn within each step
+    one_layer = algorithmic_bytes(B, HQ, HKV, D, [L + n_graph_steps for L in base], w.fp8, page)
+    NL = w.layers if w.layers > 1 else max(4, math.ceil(2 * MALL_BYTES / one_layer))
+    layer_weight = w.layers / NL  # one-layer configs: a step's time is the per-layer time
+    cap_seq = max(base) + n_graph_steps
 
     # ---- inputs, resident in HBM before anything is timed
-    g = generator(dev, w.seed)
-    kbuf, vbuf = [], []
-    for _ in range(NL):
-        kb = torch.empty((B, HKV, cap, D), dtype=torch.bfloat16, device=dev)
-        vb = torch.empty_like(kb)
-        kb[:, :, :L0] = normal((B, HKV, L0, D), g, dev, scale=w.k_scale)
-        vb[:, :, :L0] = normal((B, HKV, L0, D), g, dev)
-        kb[:, :, L0:].zero_()
-        vb[:, :, L0:].zero_()
-        kbuf.append(kb)
-        vbuf.append(vb)
-    q_all = normal((n_graph_steps, NL, B, HQ, 1, D), g, dev)
-    kn_all = normal((n_graph_steps, NL, B, HKV, 1, D), g, dev, scale=w.k_scale)
-    vn_all = normal((n_graph_steps, NL, B, HKV, 1, D), g, dev)
+    views = []
+    if not w.paged:
+        cap = (cap_seq + 63) // 64 * 64
+        for _ in range(NL):
+            kb = torch.zeros((B, HKV, cap, D), dtype=torch.bfloat16, device=dev)
+            vb = torch.zeros_like(kb)
+            for b, L in enumerate(base):
+                kb[b, :, :L] = normal((HKV, L, D), gen, dev, scale=w.k_scale)
+                vb[b, :, :L] = normal((HKV, L, D), gen, dev)
+            views.append(ops.KVCacheView(kb, vb))
+    else:
+        per_seq = [(L + n_graph_steps + page - 1) // page for L in base]
+        width, nblocks = max(per_seq), sum(per_seq)
+        for _ in range(NL):
+            perm = torch.randperm(nblocks, generator=gen, device=dev).to(torch.int32)
+            bt = torch.full((B, width), -1, dtype=torch.int32, device=dev)
+            at = 0
+            for b, n in enumerate(per_seq):
+                bt[b, :n] = perm[at : at + n]
+                at += n
+            kp = torch.zeros((nblocks, HKV, page, D), dtype=kv_dtype, device=dev)
+            vp = torch.zeros_like(kp)
+            ks = torch.zeros((nblocks, HKV, page), dtype=torch.float32, device=dev) if w.fp8 else None
+            vs = torch.zeros_like(ks) if w.fp8 else None
+            for b, L in enumerate(base):
+                src_k = normal((1, HKV, L, D), gen, dev, outlier_frac=w.outlier_frac, outlier_value=w.outlier_value)
+                src_v = normal((1, HKV, L, D), gen, dev, outlier_frac=w.outlier_frac, outlier_value=w.outlier_value)
+                ops.kv_append(ops.KVCacheView(kp, vp, ks, vs, bt[b : b + 1]), src_k, src_v,
+                              torch.zeros(1, dtype=torch.int32, device=dev))
+            views.append(ops.KVCacheView(kp, vp, ks, vs, bt))
+    q_all = normal((n_graph_steps, NL, B, HQ, 1, D), gen, dev)
+    kn_all = normal((n_graph_steps, NL, B, HKV, 1, D), gen, dev, scale=w.k_scale,
+                    outlier_frac=w.outlier_frac, outlier_value=w.outlier_value)
+    vn_all = normal((n_graph_steps, NL, B, HKV, 1, D), gen, dev,
+                    outlier_frac=w.outlier_frac, outlier_value=w.outlier_value)
     out_all = torch.zeros((n_graph_steps, NL, B, HQ, 1, D), dtype=torch.bfloat16, device=dev)
     # fused path: one length tensor for the whole step (tokens cached before it), bumped by the last layer's
-    # kernel, as a serving loop keeps it; separate path: each layer's append bumps that layer's lengths
-    shared_lens = torch.full((B,), L0, dtype=torch.int32, device=dev)
-    lens = [torch.full((B,), L0, dtype=torch.int32, device=dev) for _ in range(NL)]
-    lens0 = torch.full((B,), L0, dtype=torch.int32, device=dev)
-    views = [ops.KVCacheView(kbuf[i], vbuf[i]) for i in range(NL)]
+    # kernel when the step grows the cache, as a serving loop keeps it; separate path: each layer's append
+    # bumps that layer's lengths (and a one-step configuration restores them inside the step)
+    lens0 = torch.tensor(base, dtype=torch.int32, device=dev)
+    shared_lens = lens0.clone()
+    lens = [lens0.clone() for _ in range(NL)]
     # one split size for the whole run, planned at the longest step (the plan's workspace covers every step)
-    plan = ops.decode_plan(torch.bfloat16, B, HQ, HKV, D, L0 + n_graph_steps, 0, args.tokens_per_split)
+    plan = ops.decode_plan(kv_dtype, B, HQ, HKV, D, cap_seq, page, args.tokens_per_split)
     ws = ops.Workspace.reserve(dev, plan.workspace_bytes)
+    lo, hi = min(base), max(base)
 
     def step(s, path, kernel_events=None):
-        """One decode step: for every layer append this step's K/V row and attend (L0 + s tokens cached)."""
+        """One decode step: for every layer append this step's K/V row and attend."""
         for i in range(NL):
             if path == "fused":
                 if kernel_events is not None:
                     kernel_events[i][0].record()
                 ops.decode_attention_append(
                     q_all[s, i], views[i], kn_all[s, i], vn_all[s, i], shared_lens, sm_scale=SM_SCALE,
-                    max_seq_len=L0 + s + 1, min_seq_len=L0 + s,
-                    seq_lens_out=shared_lens if i == NL - 1 else None, out=out_all[s, i],
+                    max_seq_len=hi + s + 1, min_seq_len=lo + s,
+                    seq_lens_out=shared_lens if (growing and i == NL - 1) else None, out=out_all[s, i],
                     tokens_per_split=plan.tokens_per_split, workspace=ws,
                 )
                 if kernel_events is not None:
@@ -150,11 +214,13 @@ def main(argv=None) -> int:
                 if kernel_events is not None:
                     kernel_events[i][0].record()
                 ops.decode_attention(
-                    q_all[s, i], views[i], sm_scale=SM_SCALE, seq_lens=lens[i], max_seq_len=L0 + s + 1,
-                    min_seq_len=L0 + s + 1, out=out_all[s, i], tokens_per_split=plan.tokens_per_split, workspace=ws,
+                    q_all[s, i], views[i], sm_scale=SM_SCALE, seq_lens=lens[i], max_seq_len=hi + s + 1,
+                    min_seq_len=lo + s + 1, out=out_all[s, i], tokens_per_split=plan.tokens_per_split, workspace=ws,
                 )
                 if kernel_events is not None:
                     kernel_events[i][1].record()
+                if not growing:
+                    lens[i].copy_(lens0)
 
     def reset_lens():
         shared_lens.copy_(lens0)
@@ -179,13 +245,15 @@ def main(argv=None) -> int:
             torch.cuda.synchronize()
         return graphs
 
-    def run_steps(path, graphs, first, count):
-        if graphs is not None:
-            for s in range(first, first + count):
-                graphs[s].replay()
-        else:
-            for s in range(first, first + count):
-                step(s, path)
+    def run_steps(path, graphs, first, count, events=None):
+        for j, s in enumerate(range(first, first + count)):
+            idx = s if growing else 0
+            if graphs is not None:
+                graphs[idx].replay()
+            else:
+                step(idx, path)
+            if events is not None:
+                events[j].record()
 
     def timed(path, graphs):
         with torch.cuda.stream(stream):
@@ -195,34 +263,35 @@ def main(argv=None) -> int:
             reset_lens()
             torch.cuda.synchronize()
             ev0 = torch.cuda.Event(enable_timing=True)
-            ev1 = torch.cuda.Event(enable_timing=True)
+            evs = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
             t0 = time.perf_counter()
             ev0.record()
-            run_steps(path, graphs, 0, K)
-            ev1.record()
+            run_steps(path, graphs, 0, K, evs)
             torch.cuda.synchronize()
             t1 = time.perf_counter()
-        return ev0.elapsed_time(ev1), (t1 - t0) * 1e3
+        per_step = [ev0.elapsed_time(evs[0]) * 1e3] + [evs[j - 1].elapsed_time(evs[j]) * 1e3 for j in range(1, K)]
+        return ev0.elapsed_time(evs[-1]), (t1 - t0) * 1e3, per_step
 
     path = args.path
     other = "separate" if path == "fused" else "fused"
     graphs = capture(path) if args.mode == "graph" else None
-    gpu_ms, wall_ms = timed(path, graphs)
-    us_per_step = gpu_ms * 1e3 / K
+    gpu_ms, wall_ms, per_step_us = timed(path, graphs)
+    us_graph_step = gpu_ms * 1e3 / K  # one replay: NL layer-steps
+    us_per_step = us_graph_step * layer_weight
     other_us = None
     if args.compare_paths:
         graphs_other = capture(other) if args.mode == "graph" else None
-        other_us = timed(other, graphs_other)[0] * 1e3 / K
+        other_us = timed(other, graphs_other)[0] * 1e3 / K * layer_weight
         del graphs_other
 
-    lens_per_step = [[L0 + s + 1] * B for s in range(K)]
-    bytes_steps = [NL * algorithmic_bytes(B, HQ, HKV, D, la) for la in lens_per_step]
-    bytes_per_step = sum(bytes_steps) / K
+    lens_per_step = [[L + (s if growing else 0) + 1 for L in base] for s in range(K)]
+    layer_bytes = [algorithmic_bytes(B, HQ, HKV, D, la, w.fp8, page) for la in lens_per_step]
+    bytes_per_step = sum(layer_bytes) / K * w.layers
     gbps = bytes_per_step / (us_per_step * 1e-6) / 1e9
 
     # ---- the dominant kernel's average duration. On the fused path every launch of the timed region is that
     # kernel (NL per step, back to back in the replayed graphs), so the HIP-event time of the timed region over
-    # the number of launches is its average launch duration (launch gaps included). The separate path's
+    # the number of launches is its average launch duration (launch gaps included). The two-launch path's
     # decode launches are bracketed by events instead (queued behind a GPU sleep, so the host is ahead).
     kt_steps = min(args.kernel_timing_steps, K)
     durations = []
@@ -234,18 +303,19 @@ def main(argv=None) -> int:
                    for _ in range(kt_steps)]
             torch.cuda._sleep(int(1.0e8))
             for s in range(kt_steps):
-                step(s, path, kernel_events=evs[s])
+                step(s if growing else 0, path, kernel_events=evs[s])
             torch.cuda.synchronize()
             for s in range(kt_steps):
                 for i in range(NL):
                     durations.append(evs[s][i][0].elapsed_time(evs[s][i][1]) * 1e3)  # us
     if path == "fused":
-        dec_us = us_per_step / NL
-        dec_bytes = bytes_per_step / NL  # the fused kernel moves every algorithmic byte of the layer-step
+        dec_us = us_graph_step / NL
+        dec_bytes = sum(layer_bytes) / K  # the fused kernel moves every algorithmic byte of the layer-step
         dec_launches = K * NL
     else:
         dec_us = sum(durations) / len(durations)
-        dec_bytes = sum(decode_kernel_bytes(B, HQ, HKV, D, lens_per_step[s]) for s in range(kt_steps)) / kt_steps
+        dec_bytes = sum(decode_kernel_bytes(B, HQ, HKV, D, lens_per_step[s], w.fp8, page)
+                        for s in range(kt_steps)) / kt_steps
         dec_launches = len(durations)
     dec_gbps = dec_bytes / (dec_us * 1e-6) / 1e9
 
@@ -259,55 +329,109 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
         del src, dst
 
-    # ---- parity of the timed run's first steps against the oracle (outputs of the timed replay)
+    # ---- parity of the first steps against the oracle (outputs of a replay of the timed graphs)
     from oracle import reference_path as ref
 
+    table = ref.e4m3_decode_table() if w.fp8 else None
+
+    def cached(i, b, L):
+        """Sequence b's first L cached rows of layer instance i on the host, as the attention sees them."""
+        v = views[i]
+        if not w.paged:
+            return v.k[b, :, :L].cpu(), v.v[b, :, :L].cpu()
+        bt = v.block_table[b : b + 1].cpu()
+        k = ref.paged_gather(v.k.cpu() if not w.fp8 else v.k.cpu().view(torch.uint8), bt, [L])[0]
+        vv = ref.paged_gather(v.v.cpu() if not w.fp8 else v.v.cpu().view(torch.uint8), bt, [L])[0]
+        if w.fp8:
+            ks = ref.paged_gather(v.k_scale.cpu(), bt, [L])[0]
+            vs = ref.paged_gather(v.v_scale.cpu(), bt, [L])[0]
+            k, vv = table[k.long()] * ks[..., None], table[vv.long()] * vs[..., None]
+        return k, vv
+
     max_err = 0.0
-    check_steps = min(args.check_steps, K)
+    check_steps = min(args.check_steps, K, n_graph_steps)
     if check_steps > 0:
         with torch.cuda.stream(stream):
             reset_lens()
             torch.cuda.synchronize()
             run_steps(path, graphs, 0, check_steps)
             torch.cuda.synchronize()
-        for i in range(NL):
-            kc = kbuf[i][:, :, :L0].cpu()
-            vc = vbuf[i][:, :, :L0].cpu()
-            for s in range(check_steps):
-                kc, vc = ref.dynamic_layer_update(kc, vc, kn_all[s, i].cpu(), vn_all[s, i].cpu())
-                expect = ref.sdpa_decode(q_all[s, i].cpu(), kc, vc, SM_SCALE, HQ // HKV).float()
-                err = (out_all[s, i].float().cpu() - expect).abs().max().item()
+        seqs = list(range(B)) if B <= 8 else list(range(0, B, B // 8))[:8]
+        for i in sorted({0, NL // 2, NL - 1}):
+            for b in seqs:
+                s = check_steps - 1
+                L = base[b] + s + 1
+                k, v = cached(i, b, L)
+                expect = ref.decode_fp64(q_all[s, i, b : b + 1].cpu(), k[None], v[None], SM_SCALE, G)
+                err = (out_all[s, i, b : b + 1].double().cpu() - expect).abs().max().item()
                 max_err = max(max_err, err)
+        if not w.paged:
             # the appended rows are bit-identical to the torch.cat cache
-            assert torch.equal(kbuf[i][:, :, : L0 + check_steps].cpu().view(torch.int16), kc.view(torch.int16))
+            for i in sorted({0, NL - 1}):
+                for s in range(check_steps):
+                    for b in seqs:
+                        assert torch.equal(views[i].k[b, :, base[b] + s].cpu().view(torch.int16),
+                                           kn_all[s, i, b, :, 0].cpu().view(torch.int16))
 
-    # ---- CPU baseline: the oracle (reference PyTorch path) on the host cores, same inputs, first steps
+    # ---- CPU baseline: the oracle (reference PyTorch path) on the host cores, same inputs, first steps (a
+    # one-step configuration repeats its step from the same cache)
     cpu = None
     if args.cpu_baseline_seconds > 0:
         threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
         torch.set_num_threads(threads)
-        kc = [kbuf[i][:, :, :L0].cpu() for i in range(NL)]
-        vc = [vbuf[i][:, :, :L0].cpu() for i in range(NL)]
-        inputs = [(q_all[s].cpu(), kn_all[s].cpu(), vn_all[s].cpu()) for s in range(min(K, 64))]
+        # at most ~4 GB of cache on the host: a configuration with more times a sample of its layers and scales
+        # the time to all of them
+        layer_cache = sum(2 * L * HKV * D * 2 for L in base)
+        layers_cpu = max(1, min(w.layers, NL, (4 << 30) // layer_cache))
+        uniform = len(set(base)) == 1
+        init = []
+        for i in range(layers_cpu):
+            rows = [cached(i, b, base[b]) for b in range(B)]
+            ks = [r[0].to(torch.bfloat16) for r in rows]
+            vs = [r[1].to(torch.bfloat16) for r in rows]
+            init.append((torch.stack(ks), torch.stack(vs)) if uniform else (ks, vs))
+        state = list(init)
+
+        def cpu_step(s):
+            qs, kns, vns = q_all[s].cpu(), kn_all[s].cpu(), vn_all[s].cpu()
+            t_s = time.perf_counter()
+            for i in range(layers_cpu):
+                kc, vc = state[i]
+                if uniform:
+                    kc, vc = ref.dynamic_layer_update(kc, vc, kns[i], vns[i])
+                    ref.sdpa_decode(qs[i], kc, vc, SM_SCALE, G)
+                else:
+                    kc, vc = list(kc), list(vc)
+                    for b in range(B):
+                        kb, vb = ref.dynamic_layer_update(kc[b][None], vc[b][None], kns[i, b : b + 1],
+                                                          vns[i, b : b + 1])
+                        ref.sdpa_decode(qs[i, b : b + 1], kb, vb, SM_SCALE, G)
+                        kc[b], vc[b] = kb[0], vb[0]
+                state[i] = (kc, vc)
+            return time.perf_counter() - t_s
+
         step_times = []
         budget_t0 = time.perf_counter()
-        for s in range(len(inputs)):
-            qs, kns, vns = inputs[s]
-            t_s = time.perf_counter()
-            for i in range(NL):
-                kc[i], vc[i] = ref.dynamic_layer_update(kc[i], vc[i], kns[i], vns[i])
-                ref.sdpa_decode(qs[i], kc[i], vc[i], SM_SCALE, HQ // HKV)
-            step_times.append(time.perf_counter() - t_s)
-            if time.perf_counter() - budget_t0 > args.cpu_baseline_seconds and len(step_times) >= 2:
+        for r in range(64):
+            if not growing:
+                state[:] = init
+            step_times.append(cpu_step(r if growing else 0))
+            if len(step_times) >= 2 and (time.perf_counter() - budget_t0 > args.cpu_baseline_seconds
+                                         or (growing and r + 1 >= min(K, n_graph_steps))):
                 break
-        cpu_us = sum(step_times[1:]) / max(1, len(step_times) - 1) * 1e6 if len(step_times) > 1 else step_times[0] * 1e6
+        cpu_us = sum(step_times[1:]) / (len(step_times) - 1) * 1e6 * w.layers / layers_cpu
         cpu = {
             "value": round(cpu_us, 1),
             "unit": "us/step",
             "cores": threads,
             "kind": "port",
-            "sample": f"first {len(step_times)} of the {K} decode steps (28 layers each: torch.cat append + "
-                      f"SDPA over repeat_kv, bf16, torch {torch.__version__} eager), mean of steps 2..{len(step_times)}",
+            "sample": (f"first {len(step_times)} decode steps" if growing else f"{len(step_times)} repeats of the step")
+                      + f" of this workload ({w.layers} layer(s) each: torch.cat append + SDPA over repeat_kv"
+                      + ("" if uniform else " per sequence") + ", bf16"
+                      + (" over the dequantised fp8 cache" if w.fp8 else "")
+                      + f", torch {torch.__version__} eager), mean of {'steps' if growing else 'repeats'} "
+                      + f"2..{len(step_times)}"
+                      + ("" if layers_cpu == w.layers else f"; {layers_cpu} of the {w.layers} layers timed, scaled"),
             "cpu_model": cpu_info(),
             "cpu_capability": torch.backends.cpu.get_cpu_capability(),
             "tokens_per_s": round(B / (cpu_us * 1e-6), 1),
@@ -315,13 +439,23 @@ def main(argv=None) -> int:
 
     # HBM traffic per launch of the fused kernel, from the copy-calibrated FETCH_SIZE / WRITE_SIZE profile runs
     traffic = None
-    traffic_file = os.path.join(ROOT, "profiles", "decode_append_c2_hbm_traffic.json")
+    traffic_file = os.path.join(ROOT, "profiles", f"decode_append_{args.config}_hbm_traffic.json")
     if path == "fused" and os.path.exists(traffic_file):
         with open(traffic_file) as f:
             traffic = json.load(f)
 
+    kv_name = "fp8" if w.fp8 else "bf16"
+    describe = {
+        "c1": "B=1, 1 layer, 1024 cached, append 1 + attend over 1025",
+        "c2": "B=8, 28 layers, prefill 2048, 128 steps of append 1 + attend",
+        "c3": "B=1, 1 layer, 32768 cached, 64 steps of append 1 + attend",
+        "c4": "B=64, 28 layers, ragged lengths U{512..4096}, one step",
+        "c5": "B=32, 1 layer, ragged lengths U{256..8192}, paged (16-token pages) fp8 e4m3 + fp32 scales, one step",
+    }[args.config]
+    metric = ("us/decode-step & achieved HBM GB/s (% of 8 TB/s), B=8 L=2048 28 layers" if args.config == "c2"
+              else f"us/decode-step & achieved HBM GB/s (% of 8 TB/s), {args.config}")
     result = {
-        "metric": "us/decode-step & achieved HBM GB/s (% of 8 TB/s), B=8 L=2048 28 layers",
+        "metric": metric,
         "value": round(us_per_step, 2),
         "unit": "us/step",
         "n_gpus": 1,
@@ -331,15 +465,19 @@ def main(argv=None) -> int:
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1), K x0.5)",
+        "dtype": kv_name,
+        "data": "synthetic (seeded N(0,1)" + (", K x0.5" if w.k_scale != 1.0 else "")
+                + (", 1% outliers +-8" if w.outlier_frac else "") + ")",
         "config": {
-            "workload": "qwen3vl-2b decode: B=8, 16q/8kv heads, head_dim 128, bf16, 28 layers, prefill 2048, "
-                        "128 steps of append 1 + attend",
-            "batch": B, "layers": NL, "prefill": L0, "q_heads": HQ, "kv_heads": HKV, "head_dim": D,
+            "workload": f"qwen3vl-2b decode: 16q/8kv heads, head_dim 128, {kv_name} KV, {describe}",
+            "name": args.config, "batch": B, "layers": w.layers, "cache_instances": NL,
+            "cached_before": base[0] if w.len_range is None else [lo, hi],
+            "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "paged": w.paged, "page_size": page,
             "mode": args.mode, "path": path, "tokens_per_split": plan.tokens_per_split,
             "num_splits": plan.num_splits,
         },
+        "us_per_step_median": round(percentile(per_step_us, 0.5) * layer_weight, 2),
+        "us_per_step_p90": round(percentile(per_step_us, 0.9) * layer_weight, 2),
         "tokens_per_s": round(B / (us_per_step * 1e-6), 1),
         "hbm_bytes_per_step": int(bytes_per_step),
         "hbm_gbps": round(gbps, 1),
@@ -348,7 +486,7 @@ def main(argv=None) -> int:
         f"{other}_path_us_per_step": None if other_us is None else round(other_us, 2),
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_attn_kernel<bf16,bf16,D=128,G=2,contiguous,"
+            "kernel": f"decode_attn_kernel<bf16,{kv_name},D=128,G=2,{'paged' if w.paged else 'contiguous'},"
                       + ("append>" if path == "fused" else "no-append>"),
             "achieved": round(dec_gbps, 1),
             "peak": HBM_PEAK_GBPS,
@@ -359,7 +497,7 @@ def main(argv=None) -> int:
                 f"rocprofv3 FETCH_SIZE x{traffic['fetch_scale']} + WRITE_SIZE x{traffic['write_scale']} "
                 f"(scales from a 256 MiB copy), {traffic['profiled_lengths']}; "
                 f"{traffic['traffic_over_algorithmic']} of the algorithmic bytes at those lengths "
-                "(profiles/decode_append_c2_hbm_traffic.md)"),
+                f"(profiles/decode_append_{args.config}_hbm_traffic.md)"),
             "avg_launch_us": round(dec_us, 3),
             "avg_launch_us_event_bracketed": round(sum(durations) / len(durations), 3) if durations else None,
             "bytes_per_launch": int(dec_bytes),
