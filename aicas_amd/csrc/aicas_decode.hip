@@ -126,15 +126,24 @@ int make_layout(const aicas_kv_cache_t* c, int32_t batch, int32_t num_kv_heads, 
 // ---------------------------------------------------------------------------------------------------------
 // Dispatch tables.
 
+// Grid (row blocks, sequences). With more than one row block per sequence the length bump is a second launch
+// (the append kernel only bumps in place when one workgroup owns the sequence).
 template <int SRC, int KV>
 int launch_append_d(const aicas::AppendParams& p, int32_t batch, int32_t head_dim, hipStream_t s) {
-  const dim3 grid(batch), block(aicas::kBlockThreads);
+  const int64_t rows = 2 * int64_t{p.num_kv_heads} * p.n_new;
+  const int64_t blocks = ceil_div(rows, aicas::append_rows_per_workgroup(head_dim));
+  if (blocks > INT32_MAX) return fail(AICAS_ERR_UNSUPPORTED, "too many rows (%lld) in one append", (long long)rows);
+  const dim3 grid(static_cast<uint32_t>(blocks), batch), block(aicas::kBlockThreads);
   switch (head_dim) {
     case 16: hipLaunchKernelGGL((aicas::kv_append_kernel<SRC, KV, 16>), grid, block, 0, s, p); break;
     case 32: hipLaunchKernelGGL((aicas::kv_append_kernel<SRC, KV, 32>), grid, block, 0, s, p); break;
     case 64: hipLaunchKernelGGL((aicas::kv_append_kernel<SRC, KV, 64>), grid, block, 0, s, p); break;
     case 128: hipLaunchKernelGGL((aicas::kv_append_kernel<SRC, KV, 128>), grid, block, 0, s, p); break;
     default: return fail(AICAS_ERR_UNSUPPORTED, "head_dim %d not supported", head_dim);
+  }
+  if (blocks > 1 && p.seq_lens_out) {
+    hipLaunchKernelGGL(aicas::bump_lens_kernel, dim3(ceil_div(batch, aicas::kBlockThreads)),
+                       dim3(aicas::kBlockThreads), 0, s, p.positions, p.seq_lens_out, p.n_new, batch);
   }
   return check_launch("aicas_kv_append");
 }
@@ -311,6 +320,7 @@ int aicas_kv_append(const aicas_kv_cache_t* cache, int32_t src_dtype, const void
                     hipStream_t stream) {
   if (batch <= 0 || num_kv_heads <= 0 || n_new <= 0)
     return fail(AICAS_ERR_INVALID, "batch, num_kv_heads and n_new must be positive");
+  if (batch > 65535) return fail(AICAS_ERR_UNSUPPORTED, "batch %d exceeds 65535", batch);
   if (!valid_head_dim(head_dim)) return fail(AICAS_ERR_UNSUPPORTED, "head_dim %d not supported", head_dim);
   if (src_dtype != AICAS_DTYPE_BF16 && src_dtype != AICAS_DTYPE_FP16)
     return fail(AICAS_ERR_UNSUPPORTED, "new K/V rows must be bf16 or fp16");

@@ -6,9 +6,13 @@
 // (transformers/cache_utils.py:127-146). For fp8 caches the rows are quantized on write with one fp32
 // scale per (token, kv-head): scale = amax/448, q = e4m3(clamp(x / scale, -448, 448)).
 //
-// One workgroup per sequence. Thread 0 reads positions[b] and, after every row is written, stores
-// positions[b] + n_new into seq_lens_out[b]; because one workgroup owns a sequence, seq_lens_out may alias
-// positions (an in-place length bump that a captured HIP graph can replay step after step).
+// Grid (row blocks, sequences): a workgroup writes kAppendPasses passes of 256 / (D / 8) rows of one sequence
+// (K rows first, then V rows; head-major, then token), with every pass's source rows loaded before
+// positions[b] is read. A decode step's append (a few rows per sequence) is one workgroup per sequence, whose
+// thread 0 stores positions[b] + n_new into seq_lens_out[b] after every row is written; seq_lens_out may
+// therefore alias positions (an in-place length bump that a captured HIP graph can replay step after step).
+// When a sequence's rows need several workgroups, the host follows with bump_lens_kernel instead, so that no
+// workgroup can read a bumped position.
 #pragma once
 
 #include "common.hpp"
@@ -53,6 +57,11 @@ __device__ __forceinline__ bool append_row_offset(const KVLayout& c, int b, int 
   return true;
 }
 
+constexpr int kAppendPasses = 8;
+
+// Rows one workgroup writes.
+constexpr int append_rows_per_workgroup(int head_dim) { return kBlockThreads / (head_dim / 8) * kAppendPasses; }
+
 // SRC_DT: dtype of the incoming rows (bf16 or fp16). KV_DT: cache dtype (same as SRC_DT, or fp8).
 template <int SRC_DT, int KV_DT, int D>
 __global__ __launch_bounds__(kBlockThreads) void kv_append_kernel(AppendParams p) {
@@ -62,11 +71,12 @@ __global__ __launch_bounds__(kBlockThreads) void kv_append_kernel(AppendParams p
   constexpr int ROWS_PER_PASS = kBlockThreads / R;
 
   __shared__ int32_t s_pos;
-  const int b = blockIdx.x;
+  const int b = blockIdx.y;
   const int tid = threadIdx.x;
   const int lane = tid % R;
   const int rows_per_tensor = p.num_kv_heads * p.n_new;
   const int rows_total = 2 * rows_per_tensor;
+  const int first_row = blockIdx.x * ROWS_PER_PASS * kAppendPasses + tid / R;
 
   // Source row r (K rows first, then V rows; head-major, then token).
   auto src_row = [&](int r) -> const uint16_t* {
@@ -79,28 +89,33 @@ __global__ __launch_bounds__(kBlockThreads) void kv_append_kernel(AppendParams p
                       : static_cast<const uint16_t*>(p.v_src) + b * p.v_src_stride_b + h * p.v_src_stride_h +
                             j * p.v_src_stride_t;
   };
-  // The first pass's rows are loaded before the position is known, overlapping the two reads.
-  const int r0 = tid / R;
-  uint4 x_first = make_uint4(0u, 0u, 0u, 0u);
-  if (r0 < rows_total) x_first = *reinterpret_cast<const uint4*>(src_row(r0) + lane * VEC);
+  // Every pass's rows are loaded before the position is known, overlapping the reads.
+  uint4 x[kAppendPasses];
+#pragma unroll
+  for (int k = 0; k < kAppendPasses; ++k) {
+    const int r = first_row + k * ROWS_PER_PASS;
+    x[k] = r < rows_total ? *reinterpret_cast<const uint4*>(src_row(r) + lane * VEC) : make_uint4(0u, 0u, 0u, 0u);
+  }
   if (tid == 0) s_pos = p.positions[b];
   __syncthreads();
   const int pos = s_pos;
 
-  for (int r = r0; r < rows_total; r += ROWS_PER_PASS) {
+#pragma unroll
+  for (int k = 0; k < kAppendPasses; ++k) {
+    const int r = first_row + k * ROWS_PER_PASS;
+    if (r >= rows_total) continue;  // the whole row group (R lanes) skips together
     const int which = r / rows_per_tensor;
     const int rr = r - which * rows_per_tensor;
     const int h = rr / p.n_new;
     const int j = rr - h * p.n_new;
-    const uint4 x = (r == r0) ? x_first : *reinterpret_cast<const uint4*>(src_row(r) + lane * VEC);
     int64_t row = 0, srow = 0;
     const bool ok = append_row_offset(p.cache, b, h, pos + j, row, srow, p.status);
     if constexpr (KV_DT == kFP8E4M3) {
       float f[VEC];
-      unpack2<SRC_DT>(x.x, f[0], f[1]);
-      unpack2<SRC_DT>(x.y, f[2], f[3]);
-      unpack2<SRC_DT>(x.z, f[4], f[5]);
-      unpack2<SRC_DT>(x.w, f[6], f[7]);
+      unpack2<SRC_DT>(x[k].x, f[0], f[1]);
+      unpack2<SRC_DT>(x[k].y, f[2], f[3]);
+      unpack2<SRC_DT>(x[k].z, f[4], f[5]);
+      unpack2<SRC_DT>(x[k].w, f[6], f[7]);
       float amax = 0.0f;
 #pragma unroll
       for (int i = 0; i < VEC; ++i) amax = fmaxf(amax, fabsf(f[i]));
@@ -125,12 +140,21 @@ __global__ __launch_bounds__(kBlockThreads) void kv_append_kernel(AppendParams p
       static_assert(KV_DT == SRC_DT, "16-bit caches store the incoming rows bit for bit");
       if (ok) {
         uint16_t* dst = static_cast<uint16_t*>(which == 0 ? p.cache.k : p.cache.v) + row + lane * VEC;
-        *reinterpret_cast<uint4*>(dst) = x;
+        *reinterpret_cast<uint4*>(dst) = x[k];
       }
     }
   }
-  __syncthreads();
-  if (tid == 0 && p.seq_lens_out) p.seq_lens_out[b] = pos + p.n_new;
+  if (gridDim.x == 1) {
+    __syncthreads();
+    if (tid == 0 && p.seq_lens_out) p.seq_lens_out[b] = pos + p.n_new;
+  }
+}
+
+// seq_lens_out[b] = positions[b] + n_new, after a multi-workgroup append (positions may alias seq_lens_out).
+__global__ __launch_bounds__(kBlockThreads) void bump_lens_kernel(const int32_t* positions, int32_t* seq_lens_out,
+                                                                  int32_t n_new, int32_t batch) {
+  const int b = blockIdx.x * kBlockThreads + threadIdx.x;
+  if (b < batch) seq_lens_out[b] = positions[b] + n_new;
 }
 
 }  // namespace aicas

@@ -171,3 +171,24 @@ def test_append_rejects_bad_arguments(dev):
     with pytest.raises(_lib.AicasError):
         ops.kv_append(view, torch.zeros((1, 3, 1, 64), dtype=torch.bfloat16, device=dev),
                       torch.zeros((1, 3, 1, 64), dtype=torch.bfloat16, device=dev), pos)
+
+
+def test_prefill_sized_append_many_sequences(dev, status):
+    """A prompt-sized append (several workgroups per sequence) for more sequences than one block of the
+    length-bump launch covers, with the bumped lengths written over the positions."""
+    B, H, D, cap, n_new = 300, 2, 16, 640, 300
+    g = torch.Generator().manual_seed(41)
+    lens = torch.randint(0, cap - n_new, (B,), generator=g).tolist()
+    cache_k = _rand((B, H, cap, D), 42)
+    cache_v = _rand((B, H, cap, D), 43)
+    k_new, v_new = _rand((B, H, n_new, D), 44), _rand((B, H, n_new, D), 45)
+    exp_k, exp_v = cache_k.clone(), cache_v.clone()
+    new_lens = ref.ragged_append(exp_k, exp_v, k_new, v_new, lens)
+    gk, gv = cache_k.to(dev), cache_v.to(dev)
+    pos = torch.tensor(lens, dtype=torch.int32, device=dev)
+    ops.kv_append(ops.KVCacheView(gk, gv), k_new.to(dev), v_new.to(dev), pos, pos, status)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(gk.cpu()), _bits(exp_k))
+    assert torch.equal(_bits(gv.cpu()), _bits(exp_v))
+    assert pos.cpu().tolist() == new_lens
+    assert int(status.item()) == 0
