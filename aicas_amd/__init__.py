@@ -4,7 +4,9 @@ decoder, a drop-in for the decode path of Frun1na/AICAS's ``triton_qwen3vl`` pac
 Same import surface as ``triton_qwen3vl/__init__.py:1-16`` for this path: the backend keys,
 ``TRITON_AVAILABLE`` (False: nothing here is Triton), ``gqa_decode_attention`` and
 ``install_qwen3vl_triton_attention``; plus the HF cache (``AicasDecodeCache``) whose ``update`` runs the HIP
-append kernel. The kernels live in ``libaicas_decode.so`` (C ABI in include/aicas_decode.h).
+append kernel, and ``install_fused_decode``, which runs a text layer's whole decode step (q/k norms, rotary
+embedding, cache update, attention) in one launch. The kernels live in ``libaicas_decode.so`` (C ABI in
+include/aicas_decode.h).
 """
 
 from .backends import TEXT_BACKEND_KEY, VISION_BACKEND_KEY, text_triton_attention, vision_triton_attention
@@ -24,9 +26,13 @@ __all__ = [
 
 
 def __getattr__(name):
-    # the cache classes import transformers; load them on first use
+    # the cache classes and the attention patch import transformers; load them on first use
     if name in ("AicasDecodeCache", "AicasKVCacheLayer"):
         from . import kv_cache
 
         return getattr(kv_cache, name)
+    if name in ("install_fused_decode", "uninstall_fused_decode"):
+        from . import fused_attention
+
+        return getattr(fused_attention, name)
     raise AttributeError(name)

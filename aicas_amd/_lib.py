@@ -18,7 +18,7 @@ import torch  # noqa: F401  (must precede the library load, see above)
 LIB_NAME = "libaicas_decode.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_BF16 = 0
 DTYPE_FP16 = 1
@@ -40,6 +40,7 @@ EXPORTED_SYMBOLS = (
     "aicas_decode_plan",
     "aicas_decode_attention",
     "aicas_decode_attention_append",
+    "aicas_decode_attention_append_qk",
     "aicas_last_error",
     "aicas_abi_version",
 )
@@ -71,6 +72,23 @@ class KVCacheDesc(ctypes.Structure):
         ("scale_stride_h", ctypes.c_int64),
         ("page_size", ctypes.c_int32),
         ("kv_dtype", ctypes.c_int32),
+    ]
+
+
+class QKPrologueDesc(ctypes.Structure):
+    """Mirror of ``aicas_qk_prologue_t`` (include/aicas_decode.h)."""
+
+    _fields_ = [
+        ("q_norm_weight", ctypes.c_void_p),
+        ("k_norm_weight", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
+        ("cos", ctypes.c_void_p),
+        ("sin", ctypes.c_void_p),
+        ("cos_stride_b", ctypes.c_int64),
+        ("sin_stride_b", ctypes.c_int64),
+        ("q_out", ctypes.c_void_p),
+        ("q_out_stride_b", ctypes.c_int64),
+        ("q_out_stride_h", ctypes.c_int64),
     ]
 
 
@@ -121,6 +139,9 @@ def _bind(handle: ctypes.CDLL) -> ctypes.CDLL:
         _I32, _P, _SIZE, _P,
         _P,
     ]
+    handle.aicas_decode_attention_append_qk.restype = ctypes.c_int
+    handle.aicas_decode_attention_append_qk.argtypes = [ctypes.POINTER(KVCacheDesc), ctypes.POINTER(QKPrologueDesc)] + \
+        handle.aicas_decode_attention_append.argtypes[1:]
     return handle
 
 

@@ -14,10 +14,10 @@
 
 // Decode launchers, one translation unit per (q dtype, kv dtype) pair (decode_<q>_<kv>.hip); they return
 // nonzero for a head_dim / group size that is not instantiated.
-int launch_decode_bf16_bf16(const aicas::DecodeParams&, int, int, bool, bool, dim3, hipStream_t);
-int launch_decode_fp16_fp16(const aicas::DecodeParams&, int, int, bool, bool, dim3, hipStream_t);
-int launch_decode_bf16_fp8(const aicas::DecodeParams&, int, int, bool, bool, dim3, hipStream_t);
-int launch_decode_fp16_fp8(const aicas::DecodeParams&, int, int, bool, bool, dim3, hipStream_t);
+int launch_decode_bf16_bf16(const aicas::DecodeParams&, int, int, bool, bool, bool, dim3, hipStream_t);
+int launch_decode_fp16_fp16(const aicas::DecodeParams&, int, int, bool, bool, bool, dim3, hipStream_t);
+int launch_decode_bf16_fp8(const aicas::DecodeParams&, int, int, bool, bool, bool, dim3, hipStream_t);
+int launch_decode_fp16_fp8(const aicas::DecodeParams&, int, int, bool, bool, bool, dim3, hipStream_t);
 
 namespace {
 
@@ -149,16 +149,16 @@ int launch_append_d(const aicas::AppendParams& p, int32_t batch, int32_t head_di
 }
 
 template <bool APPEND>
-int launch_decode(const aicas::DecodeParams& p, int q_dtype, int kv_dtype, int d, int g, bool paged, dim3 grid,
-                  hipStream_t s) {
+int launch_decode(const aicas::DecodeParams& p, int q_dtype, int kv_dtype, int d, int g, bool paged, bool qk,
+                  dim3 grid, hipStream_t s) {
   using namespace aicas;
   int rc;
   if (q_dtype == kBF16) {
-    rc = kv_dtype == kFP8E4M3 ? launch_decode_bf16_fp8(p, d, g, paged, APPEND, grid, s)
-                              : launch_decode_bf16_bf16(p, d, g, paged, APPEND, grid, s);
+    rc = kv_dtype == kFP8E4M3 ? launch_decode_bf16_fp8(p, d, g, paged, APPEND, qk, grid, s)
+                              : launch_decode_bf16_bf16(p, d, g, paged, APPEND, qk, grid, s);
   } else {
-    rc = kv_dtype == kFP8E4M3 ? launch_decode_fp16_fp8(p, d, g, paged, APPEND, grid, s)
-                              : launch_decode_fp16_fp16(p, d, g, paged, APPEND, grid, s);
+    rc = kv_dtype == kFP8E4M3 ? launch_decode_fp16_fp8(p, d, g, paged, APPEND, qk, grid, s)
+                              : launch_decode_fp16_fp16(p, d, g, paged, APPEND, qk, grid, s);
   }
   if (rc) return fail(AICAS_ERR_UNSUPPORTED, "head_dim %d / GQA group size %d not supported", d, g);
   return check_launch(APPEND ? "aicas_decode_attention_append" : "aicas_decode_attention");
@@ -244,7 +244,7 @@ struct DecodeCall {
   const void* v_new;
   int64_t kn_stride_b, kn_stride_h, vn_stride_b, vn_stride_h;
   int32_t* seq_lens_out;
-  int32_t min_len;
+  const aicas_qk_prologue_t* pro;  // APPEND only; nullptr: q and the new rows are used as given
 };
 
 template <bool APPEND>
@@ -298,11 +298,81 @@ int run_decode(const DecodeCall& c, hipStream_t stream) {
   p.vn_stride_b = c.vn_stride_b;
   p.vn_stride_h = c.vn_stride_h;
   p.seq_lens_out = c.seq_lens_out;
-  p.spec_len = c.min_len > 0 ? c.min_len : 0;
+  if (APPEND && c.pro) {
+    const aicas_qk_prologue_t& pro = *c.pro;
+    const bool norm = pro.q_norm_weight || pro.k_norm_weight;
+    if ((pro.q_norm_weight && !aligned16(pro.q_norm_weight)) || (pro.k_norm_weight && !aligned16(pro.k_norm_weight)))
+      return fail(AICAS_ERR_INVALID, "norm weights must be 16-byte aligned");
+    if (norm && !(pro.eps >= 0.0f)) return fail(AICAS_ERR_INVALID, "eps must be >= 0");
+    if ((pro.cos == nullptr) != (pro.sin == nullptr)) return fail(AICAS_ERR_INVALID, "give both cos and sin, or neither");
+    if (pro.cos && (!aligned16(pro.cos) || !aligned16(pro.sin) || (pro.cos_stride_b % 8) || (pro.sin_stride_b % 8)))
+      return fail(AICAS_ERR_INVALID, "cos/sin rows must be 16-byte aligned with strides that are multiples of 8");
+    if (pro.q_out && (!aligned16(pro.q_out) || (pro.q_out_stride_b % 8) || (pro.q_out_stride_h % 8)))
+      return fail(AICAS_ERR_INVALID, "q_out must be 16-byte aligned with strides that are multiples of 8");
+    p.q_norm_w = pro.q_norm_weight;
+    p.k_norm_w = pro.k_norm_weight;
+    p.norm_eps = pro.eps;
+    p.rope_cos = pro.cos;
+    p.rope_sin = pro.sin;
+    p.rope_cos_stride_b = pro.cos_stride_b;
+    p.rope_sin_stride_b = pro.sin_stride_b;
+    p.q_out = pro.q_out;
+    p.q_out_stride_b = pro.q_out_stride_b;
+    p.q_out_stride_h = pro.q_out_stride_h;
+  }
+  // the q/k prologue variant runs when there is anything for it to do
+  const bool qk = APPEND && c.pro && (p.q_norm_w || p.k_norm_w || p.rope_cos || p.q_out);
   const int g = c.num_q_heads / c.num_kv_heads;
   const dim3 grid(pl.num_splits, c.num_kv_heads, c.batch);
-  return launch_decode<APPEND>(p, c.q_dtype, c.cache->kv_dtype, c.head_dim, g, c.cache->block_table != nullptr,
+  return launch_decode<APPEND>(p, c.q_dtype, c.cache->kv_dtype, c.head_dim, g, c.cache->block_table != nullptr, qk,
                                grid, stream);
+}
+
+int decode_append(const aicas_kv_cache_t* cache, const aicas_qk_prologue_t* pro, int32_t q_dtype, const void* q,
+                                  int64_t q_stride_b, int64_t q_stride_h, const void* k_new, int64_t k_stride_b,
+                                  int64_t k_stride_h, const void* v_new, int64_t v_stride_b, int64_t v_stride_h,
+                                  void* out, int64_t out_stride_b, int64_t out_stride_h, const int32_t* positions,
+                                  int32_t* seq_lens_out, int32_t min_len, int32_t max_seq_len, int32_t batch,
+                                  int32_t num_q_heads,
+                                  int32_t num_kv_heads, int32_t head_dim, float sm_scale, int32_t tokens_per_split,
+                                  void* workspace, size_t workspace_bytes, int32_t* status, hipStream_t stream) {
+  if (!positions) return fail(AICAS_ERR_INVALID, "positions must be non-NULL");
+  if (!k_new || !v_new) return fail(AICAS_ERR_INVALID, "k_new and v_new must be non-NULL");
+  if (!aligned16(k_new) || !aligned16(v_new) || (k_stride_b % 8) || (k_stride_h % 8) || (v_stride_b % 8) ||
+      (v_stride_h % 8))
+    return fail(AICAS_ERR_INVALID, "new K/V rows must be 16-byte aligned with strides that are multiples of 8");
+  if (max_seq_len < 1) return fail(AICAS_ERR_INVALID, "max_seq_len must count the appended token");
+  DecodeCall c{};
+  c.cache = cache;
+  c.q_dtype = q_dtype;
+  c.q = q;
+  c.q_stride_b = q_stride_b;
+  c.q_stride_h = q_stride_h;
+  c.out = out;
+  c.out_stride_b = out_stride_b;
+  c.out_stride_h = out_stride_h;
+  c.lens = positions;
+  c.uniform_len = 0;
+  (void)min_len;  // a hint the kernels do not need: they read every length on the device
+  c.bound = max_seq_len;
+  c.batch = batch;
+  c.num_q_heads = num_q_heads;
+  c.num_kv_heads = num_kv_heads;
+  c.head_dim = head_dim;
+  c.sm_scale = sm_scale;
+  c.tokens_per_split = tokens_per_split;
+  c.workspace = workspace;
+  c.workspace_bytes = workspace_bytes;
+  c.status = status;
+  c.k_new = k_new;
+  c.v_new = v_new;
+  c.kn_stride_b = k_stride_b;
+  c.kn_stride_h = k_stride_h;
+  c.vn_stride_b = v_stride_b;
+  c.vn_stride_h = v_stride_h;
+  c.seq_lens_out = seq_lens_out;
+  c.pro = pro;
+  return run_decode<true>(c, stream);
 }
 
 }  // namespace
@@ -387,7 +457,7 @@ int aicas_decode_attention(const aicas_kv_cache_t* cache, int32_t q_dtype, const
   c.out_stride_h = out_stride_h;
   c.lens = seq_lens;
   c.uniform_len = uniform_len;
-  c.min_len = seq_lens ? min_len : uniform_len;
+  (void)min_len;
   c.bound = seq_lens ? max_seq_len : uniform_len;
   c.batch = batch;
   c.num_q_heads = num_q_heads;
@@ -409,42 +479,25 @@ int aicas_decode_attention_append(const aicas_kv_cache_t* cache, int32_t q_dtype
                                   int32_t num_q_heads,
                                   int32_t num_kv_heads, int32_t head_dim, float sm_scale, int32_t tokens_per_split,
                                   void* workspace, size_t workspace_bytes, int32_t* status, hipStream_t stream) {
-  if (!positions) return fail(AICAS_ERR_INVALID, "positions must be non-NULL");
-  if (!k_new || !v_new) return fail(AICAS_ERR_INVALID, "k_new and v_new must be non-NULL");
-  if (!aligned16(k_new) || !aligned16(v_new) || (k_stride_b % 8) || (k_stride_h % 8) || (v_stride_b % 8) ||
-      (v_stride_h % 8))
-    return fail(AICAS_ERR_INVALID, "new K/V rows must be 16-byte aligned with strides that are multiples of 8");
-  if (max_seq_len < 1) return fail(AICAS_ERR_INVALID, "max_seq_len must count the appended token");
-  DecodeCall c{};
-  c.cache = cache;
-  c.q_dtype = q_dtype;
-  c.q = q;
-  c.q_stride_b = q_stride_b;
-  c.q_stride_h = q_stride_h;
-  c.out = out;
-  c.out_stride_b = out_stride_b;
-  c.out_stride_h = out_stride_h;
-  c.lens = positions;
-  c.uniform_len = 0;
-  c.min_len = min_len;
-  c.bound = max_seq_len;
-  c.batch = batch;
-  c.num_q_heads = num_q_heads;
-  c.num_kv_heads = num_kv_heads;
-  c.head_dim = head_dim;
-  c.sm_scale = sm_scale;
-  c.tokens_per_split = tokens_per_split;
-  c.workspace = workspace;
-  c.workspace_bytes = workspace_bytes;
-  c.status = status;
-  c.k_new = k_new;
-  c.v_new = v_new;
-  c.kn_stride_b = k_stride_b;
-  c.kn_stride_h = k_stride_h;
-  c.vn_stride_b = v_stride_b;
-  c.vn_stride_h = v_stride_h;
-  c.seq_lens_out = seq_lens_out;
-  return run_decode<true>(c, stream);
+  return decode_append(cache, nullptr, q_dtype, q, q_stride_b, q_stride_h, k_new, k_stride_b, k_stride_h, v_new,
+                       v_stride_b, v_stride_h, out, out_stride_b, out_stride_h, positions, seq_lens_out, min_len,
+                       max_seq_len, batch, num_q_heads, num_kv_heads, head_dim, sm_scale, tokens_per_split, workspace,
+                       workspace_bytes, status, stream);
+}
+
+int aicas_decode_attention_append_qk(const aicas_kv_cache_t* cache, const aicas_qk_prologue_t* prologue,
+                                     int32_t q_dtype, const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                     const void* k_new, int64_t k_stride_b, int64_t k_stride_h, const void* v_new,
+                                     int64_t v_stride_b, int64_t v_stride_h, void* out, int64_t out_stride_b,
+                                     int64_t out_stride_h, const int32_t* positions, int32_t* seq_lens_out,
+                                     int32_t min_len, int32_t max_seq_len, int32_t batch, int32_t num_q_heads,
+                                     int32_t num_kv_heads, int32_t head_dim, float sm_scale, int32_t tokens_per_split,
+                                     void* workspace, size_t workspace_bytes, int32_t* status, hipStream_t stream) {
+  if (!prologue) return fail(AICAS_ERR_INVALID, "prologue must be non-NULL");
+  return decode_append(cache, prologue, q_dtype, q, q_stride_b, q_stride_h, k_new, k_stride_b, k_stride_h, v_new,
+                       v_stride_b, v_stride_h, out, out_stride_b, out_stride_h, positions, seq_lens_out, min_len,
+                       max_seq_len, batch, num_q_heads, num_kv_heads, head_dim, sm_scale, tokens_per_split, workspace,
+                       workspace_bytes, status, stream);
 }
 
 }  // extern "C"

@@ -57,13 +57,9 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
   }
 }
 
-// float -> bf16 bits, round to nearest even, NaN kept quiet (same rule as torch's float->bfloat16).
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
-}
+// float -> bf16 bits, round to nearest even, NaN kept NaN (torch's float->bfloat16 rule): one
+// v_cvt_pk_bf16_f32 on gfx950.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f)); }
 
 template <int DT>
 __device__ __forceinline__ uint16_t from_f32(float f) {
@@ -71,6 +67,28 @@ __device__ __forceinline__ uint16_t from_f32(float f) {
     return f32_to_bf16(f);
   } else {
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+  }
+}
+
+// f rounded to the 16-bit type DT (nearest even) and widened back: the value a DT tensor stores for f.
+template <int DT>
+__device__ __forceinline__ float round_to(float f) {
+  if constexpr (DT == kBF16) {
+    return static_cast<float>(static_cast<__bf16>(f));
+  } else {
+    return static_cast<float>(static_cast<_Float16>(f));
+  }
+}
+
+// Two floats rounded to DT (nearest even) and packed into one dword, lo in the low half (bf16: one
+// v_cvt_pk_bf16_f32 for both).
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  if constexpr (DT == kBF16) {
+    const f32x2_t v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+  } else {
+    return static_cast<uint32_t>(from_f32<DT>(lo)) | (static_cast<uint32_t>(from_f32<DT>(hi)) << 16);
   }
 }
 

@@ -29,17 +29,21 @@
 // it then re-arms the counter to zero. Nothing ever waits on another workgroup. Sequences that need one
 // split write the output directly.
 //
-// Prologue: q, the new rows (APPEND) and, for contiguous caches whose lengths the caller bounds from below
-// (spec_len), the first chunk of each wave's static super-chunk are fetched before the lengths are read, so
-// that their latencies overlap.
+// Prologue: q, the new rows (APPEND), the q/k preparation's weights and rotary rows (QK) and, for contiguous
+// caches, the first chunk of each wave's static super-chunk are fetched before the lengths are read, so that
+// their latencies overlap; once the length is known the wave's first super-chunk is in flight before any
+// other prologue work (the q/k preparation, the new rows' staging) starts. Every load before the token loop is
+// issued on every path, and no loaded register is written before it is consumed, so that the compiler's waits
+// are exact: waiting for one buffer never drains the other.
 //
 // Fused append (APPEND): positions[b] is the length before this step; the kernel attends over
-// L_b = positions[b] + 1 tokens, takes token L_b - 1 from the new rows (k_new / v_new) instead of the cache,
-// and split 0 writes the row into the cache (quantized on write for fp8 caches,
-// with the attention then using the dequantised row, exactly what a separate append followed by attention
-// would read). Every workgroup of batch row b counts itself in when it exits (it read positions[b] at the
-// start); the last one to do so stores positions[b] + 1 to seq_lens_out[b] (which may alias positions), so
-// no workgroup can read a bumped length.
+// L_b = positions[b] + 1 tokens, of which token L_b - 1 comes from the new rows (k_new / v_new) instead of the
+// cache: every workgroup stages the rows in LDS and the wave that streams the token swaps them in before
+// consuming its chunk, and split 0 writes the row into the cache (quantized on write for fp8 caches, with the
+// attention then using the dequantised row, exactly what a separate append followed by attention would read).
+// Every workgroup of batch row b counts itself in when it exits (it read positions[b] at the start); the last
+// one to do so stores positions[b] + 1 to seq_lens_out[b] (which may alias positions), so no workgroup can read
+// a bumped length.
 #pragma once
 
 #include "common.hpp"
@@ -70,7 +74,18 @@ struct DecodeParams {
   const void* v_new;
   int64_t kn_stride_b, kn_stride_h, vn_stride_b, vn_stride_h;
   int32_t* seq_lens_out;
-  int32_t spec_len;  // caller-guaranteed lower bound on every sequence's cached length (0: none)
+  // APPEND only, optional: the model's q/k preparation applied to q and to the new K rows before use —
+  // RMSNorm over head_dim with weights q_norm_w / k_norm_w ([D], q dtype; nullptr: no norm) and the rotary
+  // embedding with rows rope_cos / rope_sin ([B, D], q dtype; nullptr: none) — and the prepared q written to
+  // q_out ([B, Hq, D], nullptr: not written).
+  const void* q_norm_w;
+  const void* k_norm_w;
+  float norm_eps;
+  const void* rope_cos;
+  const void* rope_sin;
+  int64_t rope_cos_stride_b, rope_sin_stride_b;
+  void* q_out;
+  int64_t q_out_stride_b, q_out_stride_h;
 };
 
 constexpr int kMaxBlockEntries = 2048;  // block-table entries a workgroup can hold in LDS
@@ -101,6 +116,92 @@ __device__ __forceinline__ float load_agent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The model's q/k preparation for one head row held by the R lanes of a row group, N elements per lane
+// (element d = li * N + i): RMSNorm over head_dim in fp32, rounded to the storage type DT and multiplied by the
+// weight (Qwen3VLTextRMSNorm.forward, transformers/models/qwen3_vl/modeling_qwen3_vl.py:391-404), then the
+// rotary embedding x * cos + rotate_half(x) * sin with both products and the sum rounded to DT
+// (apply_rotary_pos_emb and rotate_half, modeling_qwen3_vl.py:412-438 and :138-142). rotate_half pairs element
+// d with d +- D/2, which lies R/2 lanes away (or in the same lane when R == 1). The lane's slices of the
+// weight and of the cos/sin row come in registers (QKSlices, fetched with the kernel's first loads); `norm` and
+// `rope` say which parts apply (uniform). Every lane of the row group must take part.
+template <int N>
+struct QKSlices {
+  uint4 qw[N / 8];  // q_norm weight
+  uint4 kw[N / 8];  // k_norm weight
+  uint4 cs[N / 8];  // cos row
+  uint4 sn[N / 8];  // sin row
+};
+
+template <int DT, int D, int R, int N>
+__device__ __forceinline__ void qk_prologue(float (&x)[N], int li, const uint4 (&weight)[N / 8], bool norm,
+                                            const uint4 (&cos_s)[N / 8], const uint4 (&sin_s)[N / 8], bool rope,
+                                            float eps) {
+  static_assert(N % 8 == 0 && R * N == D, "a row is R lanes of N elements");
+  if (norm) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < N; ++i) ss = __fadd_rn(ss, __fmul_rn(x[i], x[i]));
+    ss = group_sum<R>(ss);
+    const float r = rsqrtf(__fadd_rn(ss * (1.0f / D), eps));
+#pragma unroll
+    for (int c = 0; c < N / 8; ++c) {
+      const uint32_t wv[4] = {weight[c].x, weight[c].y, weight[c].z, weight[c].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float w0, w1;
+        unpack2<DT>(wv[j], w0, w1);
+        const int i = 8 * c + 2 * j;
+        x[i] = round_to<DT>(__fmul_rn(w0, round_to<DT>(__fmul_rn(x[i], r))));
+        x[i + 1] = round_to<DT>(__fmul_rn(w1, round_to<DT>(__fmul_rn(x[i + 1], r))));
+      }
+    }
+  }
+  if (rope) {
+    float partner[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      if constexpr (R >= 2) {
+        partner[i] = __shfl_xor(x[i], R / 2);
+      } else {
+        partner[i] = x[(i + N / 2) % N];
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < N / 8; ++c) {
+      const uint32_t cv[4] = {cos_s[c].x, cos_s[c].y, cos_s[c].z, cos_s[c].w};
+      const uint32_t sv[4] = {sin_s[c].x, sin_s[c].y, sin_s[c].z, sin_s[c].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float cs[2], sn[2];
+        unpack2<DT>(cv[j], cs[0], cs[1]);
+        unpack2<DT>(sv[j], sn[0], sn[1]);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int i = 8 * c + 2 * j + e;
+          const int d = li * N + i;
+          const float rot = d < D / 2 ? -partner[i] : partner[i];
+          x[i] = round_to<DT>(__fadd_rn(round_to<DT>(__fmul_rn(x[i], cs[e])), round_to<DT>(__fmul_rn(rot, sn[e]))));
+        }
+      }
+    }
+  }
+}
+
+// A pointer into global memory that is the same in every lane, taken through readfirstlane: a per-lane choice
+// between two such pointers then selects between registers, where a choice between two kernel-argument fields
+// would otherwise become a per-lane load of the chosen field. The value is rebuilt as a global (address space
+// 1) pointer and cast back, so that accesses through it stay global_* instructions: flat_* accesses, which a
+// pointer rebuilt from an integer would otherwise get, turn every wait for a load into a wait for all of them.
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* ptr) {
+  const uint64_t v = reinterpret_cast<uint64_t>(ptr);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  __attribute__((address_space(1))) T* g =
+      reinterpret_cast<__attribute__((address_space(1))) T*>((static_cast<uint64_t>(hi) << 32) | lo);
+  return (T*)g;
+}
+
 template <int KV_DT, int U>
 struct Chunk {
   uint4 k[U];
@@ -110,8 +211,9 @@ struct Chunk {
   bool ok[U];
 };
 
-template <int Q_DT, int KV_DT, int D, int G, bool PAGED, bool APPEND>
+template <int Q_DT, int KV_DT, int D, int G, bool PAGED, bool APPEND, bool QK>
 __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams p) {
+  static_assert(APPEND || !QK, "the q/k prologue belongs to the fused append");
   using Tr = KVTraits<KV_DT>;
   constexpr int EB = Tr::kElemBytes;
   constexpr int VEC = Tr::kVec;
@@ -119,7 +221,6 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   constexpr int R = D / VEC;            // lanes per row
   constexpr int RPW = kWave / R;        // rows per wave per load
   constexpr int RPB = RPW * kWavesPerBlock;
-  constexpr int TPI = RPB * U;          // tokens per workgroup chunk
   static_assert(R >= 1 && R <= 16, "a row must fit one DPP row");
   constexpr bool FP8 = (KV_DT == kFP8E4M3);
 
@@ -187,36 +288,60 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
     return min(len, static_cast<int>(static_cast<int64_t>(s) * groups / n) * RPB);
   };
 
-  // APPEND: the new token's source rows (lanes tid < 2R; K then V), fetched now: they do not depend on the
-  // lengths.
+  // APPEND: the new token's source rows, fetched now: they do not depend on the lengths. Lanes tid < R take the
+  // K row's slices and lanes R <= tid < 2R the V row's; every other lane fetches a copy of one of them, never
+  // used, so that the load is issued on every path and the waits on it stay exact.
   uint4 new_raw[FP8 ? 2 : 1];
   if constexpr (APPEND) {
-    if (tid < 2 * R) {
-      const int c = tid % R;
-      const uint16_t* src = tid < R
-          ? static_cast<const uint16_t*>(p.k_new) + b * p.kn_stride_b + kvh * p.kn_stride_h
-          : static_cast<const uint16_t*>(p.v_new) + b * p.vn_stride_b + kvh * p.vn_stride_h;
-      new_raw[0] = *reinterpret_cast<const uint4*>(src + c * VEC);
-      if constexpr (FP8) new_raw[1] = *reinterpret_cast<const uint4*>(src + c * VEC + 8);
+    const int c = tid % R;
+    // both row addresses as uniform values before the per-lane choice (otherwise the choice becomes a per-lane
+    // load of the pointer from the kernel arguments, one more round trip ahead of every load)
+    const uint16_t* kn = uniform_ptr(static_cast<const uint16_t*>(p.k_new) + b * p.kn_stride_b + kvh * p.kn_stride_h);
+    const uint16_t* vn = uniform_ptr(static_cast<const uint16_t*>(p.v_new) + b * p.vn_stride_b + kvh * p.vn_stride_h);
+    const uint16_t* src = ((tid / R) & 1) == 0 ? kn : vn;
+    new_raw[0] = *reinterpret_cast<const uint4*>(src + c * VEC);
+    if constexpr (FP8) new_raw[1] = *reinterpret_cast<const uint4*>(src + c * VEC + 8);
+  }
+  // QK: this lane's slices of the norm weights and of the sequence's cos/sin row, fetched with the first loads
+  // so that the prologue waits on no further memory round trip. Every load is issued on every path (a part
+  // that is not given reads q's row instead, never used) so that their waits stay exact.
+  QKSlices<VEC> qks;
+  const bool qk_norm_q = QK && p.q_norm_w != nullptr;
+  const bool qk_norm_k = QK && p.k_norm_w != nullptr;
+  const bool qk_rope = QK && p.rope_cos != nullptr;
+  if constexpr (QK) {
+    const uint16_t* qrow = qb + kvh * G * p.q_stride_h;
+    const uint16_t* wq = qk_norm_q ? static_cast<const uint16_t*>(p.q_norm_w) : qrow;
+    const uint16_t* wk = qk_norm_k ? static_cast<const uint16_t*>(p.k_norm_w) : qrow;
+    const uint16_t* cr = qk_rope ? static_cast<const uint16_t*>(p.rope_cos) + b * p.rope_cos_stride_b : qrow;
+    const uint16_t* sr = qk_rope ? static_cast<const uint16_t*>(p.rope_sin) + b * p.rope_sin_stride_b : qrow;
+#pragma unroll
+    for (int c = 0; c < VEC / 8; ++c) {
+      const int e = li * VEC + 8 * c;
+      qks.qw[c] = *reinterpret_cast<const uint4*>(wq + e);
+      qks.kw[c] = *reinterpret_cast<const uint4*>(wk + e);
+      qks.cs[c] = *reinterpret_cast<const uint4*>(cr + e);
+      qks.sn[c] = *reinterpret_cast<const uint4*>(sr + e);
     }
   }
 
   // Issues the loads of rows t0 + u * RPW + row of this wave (hi >= 1). Rows at or past hi, the row `skip`
   // and rows on invalid pages come out with ok = false; they still load, from row min(t, hi - 1) (block 0 for
   // an invalid page), so that every load is issued on every path and the compiler can wait for one buffer
-  // while the other stays in flight. Their words are never let through by consume.
-  auto load_rows = [&](Chunk<KV_DT, U>& c, int t0, int hi, int skip, int first_entry) {
+  // while the other stays in flight. Their words are never let through by consume. A chunk that is not
+  // `valid` (no such chunk) loads row t_dummy of block 0 / of the sequence in every lane, all masked.
+  auto load_rows = [&](Chunk<KV_DT, U>& c, int t0, int hi, int skip, int first_entry, bool valid, int t_dummy) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int t = t0 + u * RPW + row;
-      const int tc = min(t, hi - 1);
-      bool ok = t < hi && t != skip;
+      const int tc = valid ? min(t, hi - 1) : t_dummy;
+      bool ok = valid && t < hi && t != skip;
       int64_t blk = b;
       int tin = tc;
       if constexpr (PAGED) {
         const int32_t e = s_bt[(tc >> p.page_shift) - first_entry];
         ok = ok && e >= 0;
-        blk = e >= 0 ? e : 0;
+        blk = valid && e >= 0 ? e : 0;
         tin = tc & page_mask;
       }
       const int64_t off = blk * p.cache.stride_blk + head_off + static_cast<int64_t>(tin) * p.cache.stride_t;
@@ -231,12 +356,7 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
     }
   };
 
-  // Contiguous caches whose every sequence is known (spec_len, from the caller) to hold at least spec_len
-  // tokens: the first chunk of this wave's static super-chunk is fetched before the lengths are read, so that
-  // the two latencies overlap.
   Chunk<KV_DT, U> ca, cb;
-  const bool spec_issued = !PAGED && p.spec_len > 0 && wave_slot * SCW + CW <= min(p.spec_len, limit);
-  if (spec_issued) load_rows(ca, wave_slot * SCW, limit, -1, 0);
 
   // Sequence length (cached tokens before this step's append for APPEND).
   if (tid == 0) s_len = p.seq_lens ? p.seq_lens[b] : p.uniform_len;
@@ -279,7 +399,12 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
     count_in();
     return;
   }
-
+  // APPEND, paged: the new token's block id (for the cache write), read before any cache load so that waiting
+  // for it leaves those in flight.
+  int32_t blk_new = 0;
+  if constexpr (APPEND && PAGED) {
+    blk_new = p.cache.block_table[static_cast<int64_t>(b) * p.cache.block_table_stride + (max(t_new, 0) >> p.page_shift)];
+  }
   // Schedule: striped mode unless a paged sequence's whole block-table row does not fit the LDS cache.
   bool striped = true;
   if constexpr (PAGED) striped = ((L + page_mask) >> p.page_shift) <= kMaxBlockEntries;
@@ -287,10 +412,6 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   const int stripe = n_active * kWavesPerBlock;  // striped mode: waves sharing the sequence
   const int t_begin = striped ? 0 : split_begin(split, n_active, L);
   const int t_end = striped ? L : split_begin(split + 1, n_active, L);
-  // The speculative chunk is this wave's first unit of work (striped mode, the only mode of contiguous
-  // caches); if a length falls short of spec_len after all, its rows at or past L (and the new token's row)
-  // are masked below instead of being read again.
-  const bool spec = spec_issued;
 
   // Paged caches: stage the block ids this workgroup may touch in LDS (invalid ids become -1 and their tokens
   // are skipped): the whole row in striped mode, the split's range otherwise.
@@ -299,102 +420,47 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
     first_entry = t_begin >> p.page_shift;
     const int n_ent = t_end > t_begin ? ((t_end - 1) >> p.page_shift) - first_entry + 1 : 0;
     const int32_t* bt = p.cache.block_table + static_cast<int64_t>(b) * p.cache.block_table_stride + first_entry;
-    for (int i = tid; i < n_ent; i += kBlockThreads) {
-      int32_t blk = bt[i];
-      if (blk < 0 || blk >= p.cache.num_blocks) {
-        if (p.status) atomicOr(p.status, kStatusBlockOutOfRange);
-        blk = -1;
-      }
-      s_bt[i] = blk;
+    // every load of the row first (one round trip), then the checks and the LDS writes
+    constexpr int kPer = (kMaxBlockEntries + kBlockThreads - 1) / kBlockThreads;
+    const int rounds = (n_ent + kBlockThreads - 1) / kBlockThreads;  // <= kPer
+    int32_t ent[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      if (k < rounds) ent[k] = bt[min(tid + k * kBlockThreads, n_ent - 1)];
     }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = tid + k * kBlockThreads;
+      if (k < rounds && i < n_ent) {
+        int32_t blk = ent[k];
+        if (blk < 0 || blk >= p.cache.num_blocks) {
+          if (p.status) atomicOr(p.status, kStatusBlockOutOfRange);
+          blk = -1;
+        }
+        s_bt[i] = blk;
+      }
+    }
+    __syncthreads();
   }
-  // APPEND: every workgroup stages the new token's rows in LDS as the attention must see them (whichever wave
-  // streams token t_new takes it from there); split 0 also writes them into the cache. For fp8 caches the rows
-  // are quantized on write exactly as aicas_kv_append does, and the attention uses the dequantised codes.
-  if constexpr (APPEND) {
-    if (t_new >= 0 && tid < 2 * R) {
-      const int which = tid / R;  // 0 = K, 1 = V
-      const int c = tid % R;
-      int64_t blk = b;
-      int tin = t_new;
-      bool ok = split == 0;
-      if constexpr (PAGED) {
-        blk = p.cache.block_table[static_cast<int64_t>(b) * p.cache.block_table_stride + (t_new >> p.page_shift)];
-        tin = t_new & page_mask;
-        ok = ok && blk >= 0 && blk < p.cache.num_blocks;
-      }
-      const int64_t off = blk * p.cache.stride_blk + head_off + static_cast<int64_t>(tin) * p.cache.stride_t;
-      void* dst_base = which == 0 ? p.cache.k : p.cache.v;
-      if constexpr (!FP8) {
-        if (ok) *reinterpret_cast<uint4*>(static_cast<uint16_t*>(dst_base) + off + c * VEC) = new_raw[0];
-        s_new[tid] = new_raw[0];
-      } else {
-        // VEC = 16 source elements (32 bytes) per lane -> 16 codes
-        float f[VEC];
-        const uint32_t w[8] = {new_raw[0].x, new_raw[0].y, new_raw[0].z, new_raw[0].w,
-                               new_raw[1].x, new_raw[1].y, new_raw[1].z, new_raw[1].w};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) unpack2<Q_DT>(w[i], f[2 * i], f[2 * i + 1]);
-        float amax = 0.0f;
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) amax = fmaxf(amax, fabsf(f[i]));
-        amax = group_max<R>(amax);
-        const float scale = amax / 448.0f;
-        uint32_t packed[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) {
-          uint32_t code = 0u;
-          if (scale > 0.0f) code = f32_to_e4m3(fminf(fmaxf(f[i] / scale, -448.0f), 448.0f));
-          packed[i / 4] |= code << (8 * (i % 4));
-        }
-        const uint4 codes = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-        if (ok) {
-          *reinterpret_cast<uint4*>(static_cast<uint8_t*>(dst_base) + off + c * VEC) = codes;
-          if (c == 0) {
-            const int64_t soff = blk * p.cache.scale_stride_blk + shead_off + tin;
-            (which == 0 ? p.cache.k_scale : p.cache.v_scale)[soff] = scale;
-          }
-        }
-        s_new[tid] = codes;
-        if (c == 0) s_new_scale[which] = scale;
-      }
+  // Super-chunk i of this wave starts at super_start(i) (-1: none). A chunk of rows comes from the cache; the
+  // new token's row (t_new) is masked there and swapped in from the staged rows before the chunk is consumed.
+  auto super_start = [&](int i) -> int {
+    if (striped) {
+      const int j = wave_slot + i * stripe;
+      return j < n_super ? j * SCW : -1;
     }
-  }
-  __syncthreads();
-
-  // Token t_new of a chunk comes from the staged new rows (only the chunk holding it takes this branch).
-  auto take_new_row = [&](Chunk<KV_DT, U>& c, int t0) {
-    if constexpr (APPEND) {
-      if (t_new >= t0 && t_new < t0 + CW) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          if (t0 + u * RPW + row == t_new) {
-            c.k[u] = s_new[li];
-            c.v[u] = s_new[R + li];
-            if constexpr (FP8) {
-              c.ks[u] = s_new_scale[0];
-              c.vs[u] = s_new_scale[1];
-            }
-            c.ok[u] = true;
-          }
-        }
-      }
-    }
+    const int t = t_begin + (wave + i * kWavesPerBlock) * SCW;
+    return t < t_end ? t : -1;
   };
-  // One chunk of rows: from the cache, or (token t_new) from the staged new rows.
-  auto load_chunk = [&](Chunk<KV_DT, U>& c, int t0) {
-    load_rows(c, t0, t_end, t_new, first_entry);
-    take_new_row(c, t0);
+  // The wave's first super-chunk goes out now, before the prologue work below; a wave without one loads a
+  // masked dummy (every row reads token t_begin, whose block entry is staged whenever a chunk could exist),
+  // so that every load is issued on every path and the waits on the buffers stay exact.
+  auto load_chunk = [&](Chunk<KV_DT, U>& c, int t0, bool valid) {
+    load_rows(c, valid ? t0 : t_begin, t_end, t_new, first_entry, valid, t_begin);
   };
-  if (spec) {
-    const int t0 = wave_slot * SCW;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int t = t0 + u * RPW + row;
-      ca.ok[u] = ca.ok[u] && t < L && t != t_new;
-    }
-    take_new_row(ca, t0);
-  }
+  const int sc0 = super_start(0);
+  load_chunk(ca, sc0, sc0 >= 0);
+  load_chunk(cb, sc0 + CW, sc0 >= 0);
 
   float m[G], l[G], acc[G][VEC];
 #pragma unroll
@@ -488,52 +554,186 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
     }
   };
 
-  // Token loop over super-chunks, double-buffered: chunk 1 of a super-chunk is in flight while chunk 0 is
-  // consumed, and chunk 0 of the next super-chunk while chunk 1 is.
-  {
-    int k = 0;  // super-chunks of this wave taken so far
-    auto super_start = [&](int i) -> int {
-      if (striped) {
-        const int j = wave_slot + i * stripe;
-        return j < n_super ? j * SCW : -1;
-      }
-      const int t = t_begin + (wave + i * kWavesPerBlock) * SCW;
-      return t < t_end ? t : -1;
-    };
-    const int sc = super_start(0);
-    if (sc >= 0) {
-      if (!spec) load_chunk(ca, sc);
-      load_chunk(cb, sc + CW);
-      // settle() pins the softmax state after a consume: the empty asm statements take every state register as
-      // an operand and the last one orders memory, so the whole consume (its last use of the buffer) precedes
-      // the reload that follows, and the new rows land in the registers of the old ones. Without it the
-      // compiler sinks the P.V half of a consume past the next loads and copies the buffers on every round,
-      // each copy waiting for its load. The scheduling barrier after each reload keeps its loads from sinking
-      // into the consume that follows. The last super-chunk is consumed after the loop, so that no load is
-      // issued past the end.
-      auto settle = [&]() {
+  // The prologue work that needs the length: q's preparation (QK) and the staging of the new rows (APPEND). It
+  // runs once the wave's first super-chunk is in flight, so that its latency covers the work.
+  auto prologue_work = [&]() {
+    // QK: q as the model prepares it (its loads and the slices were issued before every load of the cache, so
+    // waiting for them leaves the first super-chunk in flight; the arithmetic overlaps its latency). Split 0
+    // also writes it to q_out.
+    if constexpr (QK) {
+      {
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-          asm volatile("" : "+v"(m[h]), "+v"(l[h]));
+          float x[VEC];
+          if constexpr (!FP8) {
 #pragma unroll
-          for (int i = 0; i < VEC; ++i) asm volatile("" : "+v"(acc[h][i]));
+            for (int j = 0; j < VEC / 2; ++j) unpack2<Q_DT>(qp[h][j], x[2 * j], x[2 * j + 1]);
+          } else {
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) x[i] = qf[h][i];
+          }
+          qk_prologue<Q_DT, D, R, VEC>(x, li, qks.qw, qk_norm_q, qks.cs, qks.sn, qk_rope, p.norm_eps);
+          if constexpr (!FP8) {
+#pragma unroll
+            for (int j = 0; j < VEC / 2; ++j) qp[h][j] = pack2<Q_DT>(x[2 * j], x[2 * j + 1]);
+          } else {
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) qf[h][i] = x[i];
+          }
+          if (p.q_out && split == 0 && tid < R) {
+            uint16_t* dst = static_cast<uint16_t*>(p.q_out) + b * p.q_out_stride_b + (kvh * G + h) * p.q_out_stride_h +
+                            li * VEC;
+#pragma unroll
+            for (int c = 0; c < VEC / 8; ++c) {
+              *reinterpret_cast<uint4*>(dst + 8 * c) =
+                  make_uint4(pack2<Q_DT>(x[8 * c], x[8 * c + 1]), pack2<Q_DT>(x[8 * c + 2], x[8 * c + 3]),
+                             pack2<Q_DT>(x[8 * c + 4], x[8 * c + 5]), pack2<Q_DT>(x[8 * c + 6], x[8 * c + 7]));
+            }
+          }
         }
-        asm volatile("" ::: "memory");
-      };
-      for (int nsc = super_start(++k); nsc >= 0; nsc = super_start(++k)) {
-        consume(ca);
-        settle();
-        load_chunk(ca, nsc);
-        __builtin_amdgcn_sched_barrier(0);
-        consume(cb);
-        settle();
-        load_chunk(cb, nsc + CW);
-        __builtin_amdgcn_sched_barrier(0);
       }
-      consume(ca);
-      consume(cb);
     }
+
+    // APPEND: every workgroup stages the new token's rows in LDS as the attention must see them (whichever wave
+    // streams token t_new takes them from there); split 0 also writes them into the cache. For fp8 caches the
+    // rows are quantized on write exactly as aicas_kv_append does, and the attention uses the dequantised
+    // codes.
+    if constexpr (APPEND) {
+      if (t_new >= 0 && tid < 2 * R) {
+        const int which = tid / R;  // 0 = K, 1 = V
+        const int c = tid % R;
+        // QK: the new K row as the model prepares it (the whole K row group, lanes 0..R-1 with li == c, takes
+        // this branch)
+        if (QK && which == 0) {
+          constexpr int NW = FP8 ? 2 : 1;
+          float x[VEC];
+#pragma unroll
+          for (int n = 0; n < NW; ++n) {
+            const uint32_t w[4] = {new_raw[n].x, new_raw[n].y, new_raw[n].z, new_raw[n].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) unpack2<Q_DT>(w[j], x[8 * n + 2 * j], x[8 * n + 2 * j + 1]);
+          }
+          qk_prologue<Q_DT, D, R, VEC>(x, c, qks.kw, qk_norm_k, qks.cs, qks.sn, qk_rope, p.norm_eps);
+#pragma unroll
+          for (int n = 0; n < NW; ++n) {
+            new_raw[n] = make_uint4(pack2<Q_DT>(x[8 * n], x[8 * n + 1]), pack2<Q_DT>(x[8 * n + 2], x[8 * n + 3]),
+                                    pack2<Q_DT>(x[8 * n + 4], x[8 * n + 5]), pack2<Q_DT>(x[8 * n + 6], x[8 * n + 7]));
+          }
+        }
+        int64_t blk = b;
+        int tin = t_new;
+        bool ok = split == 0;
+        if constexpr (PAGED) {
+          blk = blk_new;
+          tin = t_new & page_mask;
+          ok = ok && blk >= 0 && blk < p.cache.num_blocks;
+        }
+        const int64_t off = blk * p.cache.stride_blk + head_off + static_cast<int64_t>(tin) * p.cache.stride_t;
+        uint8_t* const kdst = uniform_ptr(static_cast<uint8_t*>(p.cache.k));
+        uint8_t* const vdst = uniform_ptr(static_cast<uint8_t*>(p.cache.v));
+        uint8_t* dst_base = which == 0 ? kdst : vdst;
+        if constexpr (!FP8) {
+          if (ok) *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(dst_base) + off + c * VEC) = new_raw[0];
+          s_new[tid] = new_raw[0];
+        } else {
+          // VEC = 16 source elements (32 bytes) per lane -> 16 codes
+          float f[VEC];
+          const uint32_t w[8] = {new_raw[0].x, new_raw[0].y, new_raw[0].z, new_raw[0].w,
+                                 new_raw[1].x, new_raw[1].y, new_raw[1].z, new_raw[1].w};
+#pragma unroll
+          for (int i = 0; i < 8; ++i) unpack2<Q_DT>(w[i], f[2 * i], f[2 * i + 1]);
+          float amax = 0.0f;
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) amax = fmaxf(amax, fabsf(f[i]));
+          amax = group_max<R>(amax);
+          const float scale = amax / 448.0f;
+          uint32_t packed[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            uint32_t code = 0u;
+            if (scale > 0.0f) code = f32_to_e4m3(fminf(fmaxf(f[i] / scale, -448.0f), 448.0f));
+            packed[i / 4] |= code << (8 * (i % 4));
+          }
+          const uint4 codes = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+          if (ok) {
+            *reinterpret_cast<uint4*>(dst_base + off + c * VEC) = codes;
+            if (c == 0) {
+              const int64_t soff = blk * p.cache.scale_stride_blk + shead_off + tin;
+              (which == 0 ? uniform_ptr(p.cache.k_scale) : uniform_ptr(p.cache.v_scale))[soff] = scale;
+            }
+          }
+          s_new[tid] = codes;
+          if (c == 0) s_new_scale[which] = scale;
+        }
+      }
+    }
+  };
+
+  prologue_work();
+  if constexpr (APPEND) __syncthreads();  // the staged new rows are visible to every wave
+
+  // APPEND: token t_new of a chunk (skipped when the chunk was loaded) comes from the staged new rows, swapped
+  // in just before the chunk is consumed, when its loads have landed anyway (only the chunk holding it takes
+  // this branch). The token is thus attended to at its place in the stream, exactly as a separate append
+  // followed by attention would.
+  auto take_new_row = [&](Chunk<KV_DT, U>& c, int t0) {
+    if constexpr (APPEND) {
+      if (t_new >= t0 && t_new < t0 + CW) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if (t0 + u * RPW + row == t_new) {
+            c.k[u] = s_new[li];
+            c.v[u] = s_new[R + li];
+            if constexpr (FP8) {
+              c.ks[u] = s_new_scale[0];
+              c.vs[u] = s_new_scale[1];
+            }
+            c.ok[u] = true;
+          }
+        }
+      }
+    }
+  };
+  // first token of the chunk each buffer holds (far below 0 for a dummy, which holds none)
+  int ca_t0 = sc0 >= 0 ? sc0 : -(1 << 30);
+  int cb_t0 = sc0 >= 0 ? sc0 + CW : -(1 << 30);
+
+  // Token loop, double-buffered: while one buffer is consumed the other is in flight, and each is reloaded
+  // two chunks on as soon as it has been consumed. settle() pins the softmax state after a consume: the empty
+  // asm statements take every state register as an operand and the last one orders memory, so the whole
+  // consume (its last use of the buffer) precedes the reload that follows, and the new rows land in the
+  // registers of the old ones. Without it the compiler sinks the P.V half of a consume past the next loads
+  // and copies the buffers on every round, each copy waiting for its load. The scheduling barrier after each
+  // reload keeps its loads from sinking into the consume that follows. The last super-chunk is consumed after
+  // the loop, so that no load is issued past the end.
+  auto settle = [&]() {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      asm volatile("" : "+v"(m[h]), "+v"(l[h]));
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) asm volatile("" : "+v"(acc[h][i]));
+    }
+    asm volatile("" ::: "memory");
+  };
+  int k = 0;  // super-chunks of this wave taken so far
+  for (int nsc = super_start(++k); nsc >= 0; nsc = super_start(++k)) {
+    take_new_row(ca, ca_t0);
+    consume(ca);
+    settle();
+    load_chunk(ca, nsc, true);
+    ca_t0 = nsc;
+    __builtin_amdgcn_sched_barrier(0);
+    take_new_row(cb, cb_t0);
+    consume(cb);
+    settle();
+    load_chunk(cb, nsc + CW, true);
+    cb_t0 = nsc + CW;
+    __builtin_amdgcn_sched_barrier(0);
   }
+  take_new_row(ca, ca_t0);
+  consume(ca);
+  take_new_row(cb, cb_t0);
+  consume(cb);
 
   // Merge the row groups of this wave (lanes li, li + R, li + 2R, ... hold the same head_dim slice).
 #pragma unroll

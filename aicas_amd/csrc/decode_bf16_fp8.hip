@@ -1,7 +1,7 @@
 // Decode-kernel instantiations for q bf16, kv cache fp8.
 #include "decode_launch.hpp"
 
-int launch_decode_bf16_fp8(const aicas::DecodeParams& p, int d, int g, bool paged, bool append, dim3 grid,
+int launch_decode_bf16_fp8(const aicas::DecodeParams& p, int d, int g, bool paged, bool append, bool qk, dim3 grid,
                            hipStream_t s) {
-  return aicas::launch_decode_pair<aicas::kBF16, aicas::kFP8E4M3>(p, d, g, paged, append, grid, s);
+  return aicas::launch_decode_pair<aicas::kBF16, aicas::kFP8E4M3>(p, d, g, paged, append, qk, grid, s);
 }

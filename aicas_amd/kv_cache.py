@@ -160,6 +160,22 @@ class AicasKVCacheLayer(CacheLayerMixin):
         self.seq_lens.copy_(torch.tensor(lens, dtype=torch.int32), non_blocking=False)
         self.host_lens = lens
 
+    def fused_decode_step(self, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, *, sm_scale: float,
+                          qk: ops.QKPrologue | None = None) -> torch.Tensor:
+        """One decode step of this layer in one launch: append ``k_new``/``v_new`` (``[B, Hkv, 1, D]``) at every
+        sequence's length, bump the lengths on the device, and return the attention of ``q`` (``[B, Hq, 1, D]``)
+        over the grown cache. With ``qk``, q and k_new are the projections' outputs, prepared (RMSNorm, rotary
+        embedding) inside the launch as the model would."""
+        if not self.is_initialized:
+            raise RuntimeError("the cache layer is empty: prefill through update() first")
+        if max(self.host_lens) + 1 > self.view.max_tokens:
+            raise RuntimeError(f"KV cache capacity exceeded: {max(self.host_lens)} + 1 > {self.view.max_tokens} tokens")
+        out = ops.decode_attention_append(
+            q, self.view, k_new, v_new, self.seq_lens, sm_scale=sm_scale, max_seq_len=max(self.host_lens) + 1,
+            min_seq_len=min(self.host_lens), seq_lens_out=self.seq_lens, qk=qk)
+        self.host_lens = [L + 1 for L in self.host_lens]
+        return out
+
     def descriptor(self, workspace: torch.Tensor | None = None) -> AicasKV:
         uniform = len(set(self.host_lens)) == 1
         contiguous16 = self.page_size is None and not self.view.is_fp8

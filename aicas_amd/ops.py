@@ -264,10 +264,10 @@ def decode_attention(
 ) -> torch.Tensor:
     """q ``[B, Hq, 1, D]`` (or ``[B, Hq, D]``) -> out of the same shape, attending to each sequence's cache.
 
-    ``seq_lens`` (int32 ``[B]``, on device) gives per-sequence lengths; ``max_seq_len`` must bound them and
-    ``min_seq_len`` (optional) is a lower bound the caller guarantees, which lets the kernel start reading
-    K/V before it has read ``seq_lens``. Without ``seq_lens`` every sequence has ``max_seq_len`` tokens
-    (default: the cache capacity).
+    ``seq_lens`` (int32 ``[B]``, on device) gives per-sequence lengths; ``max_seq_len`` must bound them.
+    ``min_seq_len`` (optional) is a lower bound the caller may pass; the kernel reads every length on the device
+    and does not use it. Without ``seq_lens`` every sequence has ``max_seq_len`` tokens (default: the cache
+    capacity).
     """
     squeeze = q.dim() == 3
     q4 = q.unsqueeze(2) if squeeze else q
@@ -307,6 +307,51 @@ def decode_attention(
     return out
 
 
+@dataclass
+class QKPrologue:
+    """The model's q/k preparation done inside :func:`decode_attention_append` (``aicas_qk_prologue_t``):
+    RMSNorm over head_dim with ``q_norm_weight`` / ``k_norm_weight`` (``[D]``, q's dtype) and ``eps``, then the
+    rotary embedding with ``cos`` / ``sin`` rows (``[B, D]`` or ``[B, 1, D]``, q's dtype) — what
+    ``Qwen3VLTextAttention.forward`` does to the projections (transformers/models/qwen3_vl/
+    modeling_qwen3_vl.py:481-486). Any part may be None. ``q_out`` (``[B, Hq, 1, D]``) receives q as prepared."""
+
+    q_norm_weight: torch.Tensor | None = None
+    k_norm_weight: torch.Tensor | None = None
+    eps: float = 1e-6
+    cos: torch.Tensor | None = None
+    sin: torch.Tensor | None = None
+    q_out: torch.Tensor | None = None
+
+    def desc(self, B: int, Hq: int, D: int, dtype: torch.dtype) -> _lib.QKPrologueDesc:
+        d = _lib.QKPrologueDesc()
+        for name in ("q_norm_weight", "k_norm_weight"):
+            w = getattr(self, name)
+            if w is not None:
+                if w.shape != (D,) or w.dtype != dtype or not w.is_contiguous():
+                    raise AicasError(_lib.ERR_INVALID, f"{name} must be a contiguous [{D}] tensor in q's dtype")
+                setattr(d, name, w.data_ptr())
+        d.eps = float(self.eps)
+        if (self.cos is None) != (self.sin is None):
+            raise AicasError(_lib.ERR_INVALID, "give both cos and sin, or neither")
+        if self.cos is not None:
+            for name in ("cos", "sin"):
+                t = getattr(self, name)
+                t2 = t.reshape(t.shape[0], t.shape[-1]) if t.dim() == 3 and t.shape[1] == 1 else t
+                if t2.shape != (B, D) or t2.dtype != dtype or t2.stride(1) != 1:
+                    raise AicasError(_lib.ERR_INVALID, f"{name} must be [B, D] (or [B, 1, D]) in q's dtype")
+                setattr(d, name, t2.data_ptr())
+                setattr(d, f"{name}_stride_b", t2.stride(0))
+        if self.q_out is not None:
+            qo = self.q_out.unsqueeze(2) if self.q_out.dim() == 3 else self.q_out
+            if qo.shape != (B, Hq, 1, D) or qo.dtype != dtype or qo.stride(3) != 1:
+                raise AicasError(_lib.ERR_INVALID, "q_out must be [B, Hq, 1, D] in q's dtype")
+            d.q_out, d.q_out_stride_b, d.q_out_stride_h = qo.data_ptr(), qo.stride(0), qo.stride(1)
+        return d
+
+    def tensors(self):
+        return [t for t in (self.q_norm_weight, self.k_norm_weight, self.cos, self.sin, self.q_out) if t is not None]
+
+
 def decode_attention_append(
     q: torch.Tensor,
     cache: KVCacheView,
@@ -322,11 +367,13 @@ def decode_attention_append(
     tokens_per_split: int = 0,
     workspace: torch.Tensor | None = None,
     status: torch.Tensor | None = None,
+    qk: QKPrologue | None = None,
 ) -> torch.Tensor:
     """One decode step in one launch: append ``k_new``/``v_new`` (``[B, Hkv, 1, D]`` or ``[B, Hkv, D]``) at
     ``positions[b]`` and attend over ``positions[b] + 1`` tokens. ``seq_lens_out[b] = positions[b] + 1`` (it
-    may be ``positions`` itself). ``max_seq_len`` bounds ``positions[b] + 1``; ``min_seq_len`` (optional) is a
-    lower bound on every ``positions[b]``."""
+    may be ``positions`` itself). ``max_seq_len`` bounds ``positions[b] + 1``; ``min_seq_len`` (optional, unused
+    by the kernel) is a lower bound on every ``positions[b]``. With ``qk``, q and ``k_new`` are the projections' outputs and are
+    normalised and rotated as the model does before use (``aicas_decode_attention_append_qk``)."""
     squeeze = q.dim() == 3
     q4 = q.unsqueeze(2) if squeeze else q
     if q4.dim() != 4 or q4.shape[2] != 1 or q4.stride(3) != 1:
@@ -344,7 +391,8 @@ def decode_attention_append(
         raise AicasError(_lib.ERR_INVALID, "positions must be a contiguous int32 tensor with one entry per sequence")
     if seq_lens_out is not None and (seq_lens_out.dtype != torch.int32 or not seq_lens_out.is_contiguous()):
         raise AicasError(_lib.ERR_INVALID, "seq_lens_out must be a contiguous int32 tensor")
-    _require_gpu(cache.k, q4, kn, vn, positions, seq_lens_out, out, workspace, status)
+    _require_gpu(cache.k, q4, kn, vn, positions, seq_lens_out, out, workspace, status,
+                 *(qk.tensors() if qk is not None else ()))
     if out is None:
         out = torch.empty((B, Hq, 1, D), dtype=q.dtype, device=q.device)
     out4 = out.unsqueeze(2) if out.dim() == 3 else out
@@ -357,15 +405,16 @@ def decode_attention_append(
     if workspace is None:
         workspace = Workspace.get(cache.device, pl.workspace_bytes)
     desc = cache.desc()
-    check(
-        _lib.lib().aicas_decode_attention_append(
-            ctypes.byref(desc), dtype_code(q.dtype), q4.data_ptr(), q4.stride(0), q4.stride(1),
+    args = (dtype_code(q.dtype), q4.data_ptr(), q4.stride(0), q4.stride(1),
             kn.data_ptr(), kn.stride(0), kn.stride(1), vn.data_ptr(), vn.stride(0), vn.stride(1),
             out4.data_ptr(), out4.stride(0), out4.stride(1),
             positions.data_ptr(), _ptr(seq_lens_out), int(min_seq_len), int(max_seq_len),
             B, Hq, cache.num_kv_heads, D, float(sm_scale),
             pl.tokens_per_split, workspace.data_ptr(), workspace.numel(), _ptr(status),
-            _stream(cache.device),
-        )
-    )
+            _stream(cache.device))
+    if qk is None:
+        check(_lib.lib().aicas_decode_attention_append(ctypes.byref(desc), *args))
+    else:
+        pro = qk.desc(B, Hq, D, q.dtype)
+        check(_lib.lib().aicas_decode_attention_append_qk(ctypes.byref(desc), ctypes.byref(pro), *args))
     return out

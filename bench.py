@@ -6,7 +6,10 @@ each run, for every layer, one KV append (1 token per sequence) and one decode a
 cache. A step is therefore 28 x {append, attend}; --steps K times exactly K steps (K=128 is one full
 128-token generation), after --warmup W untimed steps. Cache lengths are reset between warmup and timing.
 The default path runs each layer's append + attend as one launch (aicas_decode_attention_append); the
-two-launch path (aicas_kv_append, then aicas_decode_attention) is timed beside it and reported.
+two-launch path (aicas_kv_append, then aicas_decode_attention) is timed beside it and reported, and so is the
+fused launch with the model's q/k preparation inside it (aicas_decode_attention_append_qk: q/k RMSNorm and the
+rotary embedding applied to the raw projections, prepared q written out), which does more than the headline
+step and is never the value.
 
 The other seeded configurations of aicas_amd.workloads run with --config:
   c1  B=1, 1 layer, 1024 cached, one step (append at 1024, attend over 1025), repeated;
@@ -57,6 +60,8 @@ def parse_args(argv=None):
     p.add_argument("--path", choices=("fused", "separate"), default="fused",
                    help="fused: one launch per layer appends and attends; separate: append kernel + decode kernel")
     p.add_argument("--compare-paths", type=int, default=1, help="also time the other path (reported, not the value)")
+    p.add_argument("--compare-qk", type=int, default=1,
+                   help="also time the fused path with the q/k RMSNorm + rotary prologue (reported, not the value)")
     p.add_argument("--tokens-per-split", type=int, default=0, help="0 = the library's plan")
     p.add_argument("--cpu-baseline-seconds", type=float, default=15.0,
                    help="approximate CPU time budget for the oracle baseline (0 disables it)")
@@ -118,8 +123,8 @@ def percentile(xs, p):
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path does not shard "
-              "across GPUs here; see DESIGN.md for how it would).", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: each GPU serves its own "
+              "sequences (or kv heads), so the step does not shard across GPUs here.", file=sys.stderr)
         return 2
 
     import torch
@@ -184,6 +189,19 @@ def main(argv=None) -> int:
     vn_all = normal((n_graph_steps, NL, B, HKV, 1, D), gen, dev,
                     outlier_frac=w.outlier_frac, outlier_value=w.outlier_value)
     out_all = torch.zeros((n_graph_steps, NL, B, HQ, 1, D), dtype=torch.bfloat16, device=dev)
+    # q/k preparation inputs for the fused_qk path: per-layer norm weights, per-step rotary rows of the text
+    # positions (the default rotary base 5e6 over head_dim), prepared q written per layer
+    qk_all = None
+    if args.compare_qk:
+        qn_w = 1 + 0.1 * normal((NL, D), gen, dev)
+        kn_w = 1 + 0.1 * normal((NL, D), gen, dev)
+        inv_freq = 1.0 / (5.0e6 ** (torch.arange(0, D, 2, dtype=torch.float32, device=dev) / D))
+        pos = torch.tensor(base, dtype=torch.float32, device=dev)[None, :] + torch.arange(
+            n_graph_steps, dtype=torch.float32, device=dev)[:, None]
+        ang = pos[..., None] * inv_freq
+        ang = torch.cat([ang, ang], -1)  # [steps, B, D]
+        qk_all = (qn_w, kn_w, ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16),
+                  torch.zeros((NL, B, HQ, 1, D), dtype=torch.bfloat16, device=dev))
     # fused path: one length tensor for the whole step (tokens cached before it), bumped by the last layer's
     # kernel when the step grows the cache, as a serving loop keeps it; separate path: each layer's append
     # bumps that layer's lengths (and a one-step configuration restores them inside the step)
@@ -198,14 +216,19 @@ def main(argv=None) -> int:
     def step(s, path, kernel_events=None):
         """One decode step: for every layer append this step's K/V row and attend."""
         for i in range(NL):
-            if path == "fused":
+            if path in ("fused", "fused_qk"):
+                qk = None
+                if path == "fused_qk":
+                    qn_w, kn_w, cos_all, sin_all, q_prep = qk_all
+                    qk = ops.QKPrologue(q_norm_weight=qn_w[i], k_norm_weight=kn_w[i], eps=1e-6,
+                                        cos=cos_all[s], sin=sin_all[s], q_out=q_prep[i])
                 if kernel_events is not None:
                     kernel_events[i][0].record()
                 ops.decode_attention_append(
                     q_all[s, i], views[i], kn_all[s, i], vn_all[s, i], shared_lens, sm_scale=SM_SCALE,
                     max_seq_len=hi + s + 1, min_seq_len=lo + s,
                     seq_lens_out=shared_lens if (growing and i == NL - 1) else None, out=out_all[s, i],
-                    tokens_per_split=plan.tokens_per_split, workspace=ws,
+                    tokens_per_split=plan.tokens_per_split, workspace=ws, qk=qk,
                 )
                 if kernel_events is not None:
                     kernel_events[i][1].record()
@@ -283,6 +306,11 @@ def main(argv=None) -> int:
         graphs_other = capture(other) if args.mode == "graph" else None
         other_us = timed(other, graphs_other)[0] * 1e3 / K * layer_weight
         del graphs_other
+    qk_us = None
+    if args.compare_qk:
+        graphs_qk = capture("fused_qk") if args.mode == "graph" else None
+        qk_us = timed("fused_qk", graphs_qk)[0] * 1e3 / K * layer_weight
+        del graphs_qk
 
     lens_per_step = [[L + (s if growing else 0) + 1 for L in base] for s in range(K)]
     layer_bytes = [algorithmic_bytes(B, HQ, HKV, D, la, w.fp8, page) for la in lens_per_step]
@@ -484,6 +512,7 @@ def main(argv=None) -> int:
         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
         "wall_ms": round(wall_ms, 3),
         f"{other}_path_us_per_step": None if other_us is None else round(other_us, 2),
+        "fused_qk_path_us_per_step": None if qk_us is None else round(qk_us, 2),
         "roofline": {
             "bound": "hbm",
             "kernel": f"decode_attn_kernel<bf16,{kv_name},D=128,G=2,{'paged' if w.paged else 'contiguous'},"

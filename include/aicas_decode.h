@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define AICAS_ABI_VERSION 3
+#define AICAS_ABI_VERSION 4
 
 /* Element types. */
 #define AICAS_DTYPE_BF16 0
@@ -121,9 +121,8 @@ int aicas_decode_plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int3
  * cache must have kv_dtype == q_dtype. max_seq_len must bound every L_b: longer sequences are clamped and
  * AICAS_STATUS_LEN_CLAMPED is set. An empty sequence (L_b == 0) yields zeros. head_dim in {16, 32, 64, 128},
  * G in {1, 2, 4, 8}. tokens_per_split as from aicas_decode_plan (0 = automatic). min_len is a lower bound on every
- * L_b that the caller guarantees (0 if unknown; ignored when seq_lens is NULL): it lets contiguous-cache
- * kernels start reading K/V before they have read seq_lens. A min_len above some L_b only costs that sequence
- * the early start (reads stay inside the cache, the result is unchanged).
+ * L_b that the caller may pass (0 if unknown). The kernels read every length on the device before their first
+ * cache read and do not use it; results never depend on it.
  * Replaces: triton_qwen3vl/gqa_decode_attention.py:46-141, :268-327; dujunbaoV1/native_cuda_ops/
  * decode_q1_gqa.cpp:73-95; new KV cache/evaluation_wrapper.py:248-265.
  */
@@ -142,7 +141,7 @@ int aicas_decode_attention(const aicas_kv_cache_t* cache, int32_t q_dtype, const
  * aicas_kv_append followed by aicas_decode_attention would give. If seq_lens_out is not NULL,
  * seq_lens_out[b] = positions[b] + 1 is stored once every workgroup has read positions[b]; it may alias
  * positions. max_seq_len must bound positions[b] + 1; min_len (0 if unknown) is a lower bound on every
- * positions[b], as for aicas_decode_attention. A token with no slot left in the cache is dropped and
+ * positions[b], unused as for aicas_decode_attention. A token with no slot left in the cache is dropped and
  * AICAS_STATUS_APPEND_OVERFLOW is set. The workspace must come from aicas_decode_plan with the same shapes.
  * Replaces the pair Qwen3VLTextAttention.forward issues per layer and step
  * (transformers/models/qwen3_vl/modeling_qwen3_vl.py:487-503): past_key_values.update (cache_utils.py:127-146)
@@ -156,6 +155,50 @@ int aicas_decode_attention_append(const aicas_kv_cache_t* cache, int32_t q_dtype
                                   int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, float sm_scale,
                                   int32_t tokens_per_split, void* workspace, size_t workspace_bytes, int32_t* status,
                                   hipStream_t stream);
+
+/*
+ * The model's q/k preparation, fused into aicas_decode_attention_append_qk. Every pointer may be NULL (that
+ * step is skipped); element types are q_dtype's, head_dim strides 1.
+ *   q_norm_weight, k_norm_weight  [head_dim]: RMSNorm over head_dim of q and of the new K rows: x / sqrt(
+ *                                 mean(x^2) + eps) in fp32, rounded to q_dtype, times the weight, rounded;
+ *   cos, sin                      [B, head_dim] rows (strides cos_stride_b / sin_stride_b elements, multiples
+ *                                 of 8): rotary embedding x * cos + rotate_half(x) * sin, rotate_half(x) =
+ *                                 (-x[D/2:], x[:D/2]), each product and the sum rounded to q_dtype;
+ *   q_out                         [B, Hq, head_dim] (strides in elements, multiples of 8): receives q as
+ *                                 prepared.
+ * Pointers are 16-byte aligned.
+ */
+typedef struct aicas_qk_prologue {
+  const void* q_norm_weight;
+  const void* k_norm_weight;
+  float eps;
+  const void* cos;
+  const void* sin;
+  int64_t cos_stride_b;
+  int64_t sin_stride_b;
+  void* q_out;
+  int64_t q_out_stride_b;
+  int64_t q_out_stride_h;
+} aicas_qk_prologue_t;
+
+/*
+ * aicas_decode_attention_append with the model's q/k preparation done in the same launch: q (the query
+ * projection's output) and k_new (the key projection's output) are RMS-normalised and rotated as the
+ * prologue says before the rows are written and attended to; v_new is written as given. One launch per layer
+ * and decode step in place of the q/k norms, the rotary embedding, the cache update and the attention.
+ * Replaces: transformers/models/qwen3_vl/modeling_qwen3_vl.py:481-488 (q_norm, k_norm,
+ * apply_rotary_pos_emb, past_key_values.update) followed by the text attention function
+ * (triton_qwen3vl/backends.py:207-227); the same fused step as dujunbaoV1/native_cuda_ops/
+ * decode_q1_gqa_kernel.cu:376-480 plus the attention.
+ */
+int aicas_decode_attention_append_qk(const aicas_kv_cache_t* cache, const aicas_qk_prologue_t* prologue,
+                                     int32_t q_dtype, const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                     const void* k_new, int64_t k_stride_b, int64_t k_stride_h, const void* v_new,
+                                     int64_t v_stride_b, int64_t v_stride_h, void* out, int64_t out_stride_b,
+                                     int64_t out_stride_h, const int32_t* positions, int32_t* seq_lens_out,
+                                     int32_t min_len, int32_t max_seq_len, int32_t batch, int32_t num_q_heads,
+                                     int32_t num_kv_heads, int32_t head_dim, float sm_scale, int32_t tokens_per_split,
+                                     void* workspace, size_t workspace_bytes, int32_t* status, hipStream_t stream);
 
 /* Message describing the last failure on the calling thread ("" if none). */
 const char* aicas_last_error(void);

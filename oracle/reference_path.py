@@ -221,3 +221,39 @@ def paged_scatter_rows(
     """Write rows [Hkv, ...] of token t of sequence b into the pool."""
     page = pool.shape[2]
     pool[block_table[b, t // page].long(), :, t % page] = rows
+
+
+# ------------------------------------------------------------------------- q/k preparation (norm + RoPE)
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """Qwen3VLTextRMSNorm.forward (transformers/models/qwen3_vl/modeling_qwen3_vl.py:391-404): over the last
+    axis in float32, x / sqrt(mean(x^2) + eps), cast back to x's dtype, times the weight (in that dtype)."""
+    dtype = x.dtype
+    xf = x.to(torch.float32)
+    var = xf.pow(2).mean(-1, keepdim=True)
+    return weight * (xf * torch.rsqrt(var + eps)).to(dtype)
+
+
+def rotate_half(x: torch.Tensor) -> torch.Tensor:
+    """modeling_qwen3_vl.py:138-142: (x1, x2) -> (-x2, x1) over the halves of the last axis."""
+    h = x.shape[-1] // 2
+    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+
+def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """apply_rotary_pos_emb (modeling_qwen3_vl.py:412-438) for one of q/k: x [B, H, S, D], cos/sin [B, S, D]
+    broadcast over the heads; x * cos + rotate_half(x) * sin in x's dtype (each product and the sum rounded)."""
+    cos, sin = cos.unsqueeze(1), sin.unsqueeze(1)
+    return (x * cos) + (rotate_half(x) * sin)
+
+
+def prepare_qk(q: torch.Tensor, k: torch.Tensor, q_w, k_w, eps: float, cos, sin):
+    """What Qwen3VLTextAttention.forward does to the q/k projections before the cache update and the attention
+    (modeling_qwen3_vl.py:481-486): q_norm / k_norm, then the rotary embedding. q [B, Hq, S, D], k [B, Hkv, S, D];
+    a None weight or cos skips that step."""
+    if q_w is not None:
+        q = rms_norm(q, q_w, eps)
+    if k_w is not None:
+        k = rms_norm(k, k_w, eps)
+    if cos is not None:
+        q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+    return q, k

@@ -47,23 +47,25 @@ def test_constants_match_header():
         assert re.search(rf"#define {name} {value}\b", text), name
 
 
-def test_cache_descriptor_layout_matches_header(tmp_path):
-    """The ctypes mirror of aicas_kv_cache_t has the C compiler's layout (sizeof and every offsetof)."""
-    fields = [f[0] for f in _lib.KVCacheDesc._fields_]
+@pytest.mark.parametrize("ctype, struct", [("aicas_kv_cache_t", _lib.KVCacheDesc),
+                                           ("aicas_qk_prologue_t", _lib.QKPrologueDesc)])
+def test_descriptor_layouts_match_header(tmp_path, ctype, struct):
+    """The ctypes mirrors of the ABI's structs have the C compiler's layout (sizeof and every offsetof)."""
+    fields = [f[0] for f in struct._fields_]
     src = tmp_path / "layout.c"
     src.write_text(
         '#include <stdio.h>\n#include <stddef.h>\n#include "aicas_decode.h"\nint main(void) {\n'
-        + '  printf("%zu\\n", sizeof(aicas_kv_cache_t));\n'
-        + "".join(f'  printf("%zu\\n", offsetof(aicas_kv_cache_t, {f}));\n' for f in fields)
+        + f'  printf("%zu\\n", sizeof({ctype}));\n'
+        + "".join(f'  printf("%zu\\n", offsetof({ctype}, {f}));\n' for f in fields)
         + "  return 0;\n}\n")
     exe = tmp_path / "layout"
     rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
     subprocess.run(["gcc", "-D__HIP_PLATFORM_AMD__", "-I", os.path.dirname(HEADER), "-I", os.path.join(rocm, "include"),
                     str(src), "-o", str(exe)], check=True)
     values = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
-    assert values[0] == ctypes.sizeof(_lib.KVCacheDesc)
+    assert values[0] == ctypes.sizeof(struct)
     for f, off in zip(fields, values[1:]):
-        assert getattr(_lib.KVCacheDesc, f).offset == off, f
+        assert getattr(struct, f).offset == off, f
 
 
 def _plan(kv_dtype, B, Hq, Hkv, D, L, page=0, hint=0):
@@ -194,3 +196,27 @@ def test_fused_entry_argument_errors():
         ctypes.byref(d), _lib.DTYPE_BF16, FAKE, 16 * 128, 128, None, 8 * 128, 128, FAKE, 8 * 128, 128,
         FAKE + 4096, 16 * 128, 128, FAKE, None, 0, 10, 1, 16, 8, 128, 0.1, 0, FAKE, 1 << 20, None, None)
     assert rc == _lib.ERR_INVALID and "k_new" in _last_error()
+
+
+@no_gpu_only
+def test_fused_qk_entry_argument_errors():
+    lib = _lib.lib()
+    d = _desc()
+
+    def call(pro):
+        return lib.aicas_decode_attention_append_qk(
+            ctypes.byref(d), pro, _lib.DTYPE_BF16, FAKE, 16 * 128, 128, FAKE, 8 * 128, 128, FAKE, 8 * 128, 128,
+            FAKE + 4096, 16 * 128, 128, FAKE, None, 0, 10, 1, 16, 8, 128, 0.1, 0, FAKE + (1 << 26), 1 << 20, None,
+            None)
+
+    assert call(None) == _lib.ERR_INVALID and "prologue" in _last_error()
+    pro = _lib.QKPrologueDesc()
+    pro.cos = FAKE
+    assert call(ctypes.byref(pro)) == _lib.ERR_INVALID and "cos and sin" in _last_error()
+    pro = _lib.QKPrologueDesc()
+    pro.q_norm_weight = FAKE + 2
+    assert call(ctypes.byref(pro)) == _lib.ERR_INVALID and "aligned" in _last_error()
+    pro = _lib.QKPrologueDesc()
+    pro.q_norm_weight = FAKE
+    pro.eps = -1.0
+    assert call(ctypes.byref(pro)) == _lib.ERR_INVALID and "eps" in _last_error()

@@ -227,3 +227,66 @@ def test_lse_merge_equals_single_pass(splits):
     k2[95] = q / q.norm() * (40.0 / (32 ** -0.5 * q.norm()))
     ms, ls, accs = ref.split_partials(q, k2, v, 32 ** -0.5, splits)
     assert (ref.merge_partials(ms, ls, accs) - v[95]).abs().max() < 1e-6
+
+
+# ------------------------------------------------------------------------- q/k preparation (norm + RoPE)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_qk_preparation_matches_transformers_modules(dtype):
+    """rms_norm / apply_rope / prepare_qk against the library routines the reference path calls:
+    transformers' Qwen3VLTextRMSNorm and apply_rotary_pos_emb, with cos/sin from its Qwen3VLTextRotaryEmbedding
+    (interleaved M-RoPE, text positions) — bit for bit."""
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLTextConfig
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import (
+        Qwen3VLTextRMSNorm, Qwen3VLTextRotaryEmbedding, apply_rotary_pos_emb)
+
+    g = torch.Generator().manual_seed(3)
+    B, Hq, Hkv, D = 3, 16, 8, 128
+    cfg = Qwen3VLTextConfig(hidden_size=256, num_attention_heads=Hq, num_key_value_heads=Hkv, head_dim=D)
+    qn, kn = Qwen3VLTextRMSNorm(D, eps=1e-6), Qwen3VLTextRMSNorm(D, eps=1e-6)
+    with torch.no_grad():
+        qn.weight.copy_(1 + 0.1 * torch.randn(D, generator=g))
+        kn.weight.copy_(1 + 0.1 * torch.randn(D, generator=g))
+    qn, kn = qn.to(dtype), kn.to(dtype)
+    q = (3 * torch.randn((B, 1, Hq, D), generator=g)).to(dtype)
+    k = (3 * torch.randn((B, 1, Hkv, D), generator=g)).to(dtype)
+    pos = torch.tensor([[5], [1000], [31000]])
+    cos, sin = Qwen3VLTextRotaryEmbedding(cfg)(q, pos)
+    with torch.no_grad():
+        hq, hk = apply_rotary_pos_emb(qn(q).transpose(1, 2), kn(k).transpose(1, 2), cos, sin)
+        oq, ok = ref.prepare_qk(q.transpose(1, 2), k.transpose(1, 2), qn.weight, kn.weight, 1e-6, cos, sin)
+        assert torch.equal(ref.rms_norm(q, qn.weight, 1e-6), qn(q))
+    assert torch.equal(oq, hq) and torch.equal(ok, hk)
+
+
+def test_rope_is_the_pairwise_rotation():
+    """In float64, x * cos + rotate_half(x) * sin with cos/sin = cat(c, c) / cat(s, s) rotates each pair
+    (x_j, x_{j+D/2}) by the angle of frequency j, so it keeps every pair's length; angle 0 is the identity."""
+    g = torch.Generator().manual_seed(4)
+    B, H, D = 2, 3, 64
+    x = torch.randn((B, H, 1, D), generator=g, dtype=torch.float64)
+    theta = torch.rand((B, 1, D // 2), generator=g, dtype=torch.float64) * 2 * math.pi
+    cos, sin = torch.cat([theta.cos()] * 2, -1), torch.cat([theta.sin()] * 2, -1)
+    y = ref.apply_rope(x, cos, sin)
+    a, b_ = x[..., : D // 2], x[..., D // 2 :]
+    t = theta.unsqueeze(1)
+    assert torch.allclose(y[..., : D // 2], a * t.cos() - b_ * t.sin(), atol=1e-12)
+    assert torch.allclose(y[..., D // 2 :], b_ * t.cos() + a * t.sin(), atol=1e-12)
+    assert torch.allclose(y[..., : D // 2] ** 2 + y[..., D // 2 :] ** 2, a ** 2 + b_ ** 2, atol=1e-12)
+    zero = torch.zeros_like(theta)
+    assert torch.equal(ref.apply_rope(x, torch.cat([zero.cos()] * 2, -1), torch.cat([zero.sin()] * 2, -1)), x)
+
+
+def test_rms_norm_closed_forms():
+    """A constant row c gives weight * c / sqrt(c^2 + eps); with unit weight any row comes out with mean square
+    1 / (1 + eps / mean(x^2)); scaling the row does not change it when eps = 0. (The norm is computed in float32
+    whatever the input type, as the model's module does, hence float32 tolerances.)"""
+    D, eps = 128, 1e-6
+    w = torch.linspace(0.5, 1.5, D, dtype=torch.float64)
+    for c in (-3.0, 1e-4, 7.5):
+        y = ref.rms_norm(torch.full((D,), c, dtype=torch.float64), w, eps)
+        assert torch.allclose(y, w * c / math.sqrt(c * c + eps), rtol=1e-6)
+    x = torch.randn((5, D), generator=torch.Generator().manual_seed(6), dtype=torch.float64)
+    ms = x.pow(2).mean(-1)
+    y = ref.rms_norm(x, torch.ones(D, dtype=torch.float64), eps)
+    assert torch.allclose(y.pow(2).mean(-1), 1 / (1 + eps / ms), rtol=1e-6)
+    assert torch.allclose(ref.rms_norm(37.0 * x, w, 0.0), ref.rms_norm(x, w, 0.0), rtol=1e-6)
