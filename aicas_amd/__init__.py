@@ -5,7 +5,8 @@ Same import surface as ``triton_qwen3vl/__init__.py:1-16`` for this path: the ba
 ``TRITON_AVAILABLE`` (False: nothing here is Triton), ``gqa_decode_attention`` and
 ``install_qwen3vl_triton_attention``; plus the HF cache (``AicasDecodeCache``) whose ``update`` runs the HIP
 append kernel, and ``install_fused_decode``, which runs a text layer's whole decode step (q/k norms, rotary
-embedding, cache update, attention) in one launch. The kernels live in ``libaicas_decode.so`` (C ABI in
+embedding, cache update, attention) in one launch, and ``AicasGraphDecodeRunner``, which captures a whole
+decode step of the text model as a HIP graph. The kernels live in ``libaicas_decode.so`` (C ABI in
 include/aicas_decode.h).
 """
 
@@ -35,4 +36,8 @@ def __getattr__(name):
         from . import fused_attention
 
         return getattr(fused_attention, name)
+    if name == "AicasGraphDecodeRunner":
+        from . import graph_runner
+
+        return graph_runner.AicasGraphDecodeRunner
     raise AttributeError(name)
