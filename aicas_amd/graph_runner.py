@@ -10,8 +10,11 @@ fixed-size K/V and needs a host-maintained boolean visibility mask over the whol
 about the length is baked into the graph, so one capture serves every step until the cache is full, for
 contiguous, paged and fp8 caches alike.
 
-The captured step is embed_tokens → rotary_emb → every decoder layer → norm → lm_head → argmax, as the
-reference's ``_run_step`` (:272-337) does for its non-native path.
+The captured step is embed_tokens → rotary_emb → every decoder layer → norm → lm_head, as the reference's
+``_run_step`` (:272-337) does for its non-native path; the argmax over the vocabulary runs right after each
+replay, on the same stream, outside the graph: torch reduces a 152k-wide row across workgroups and zeroes
+their semaphores with hipMemsetAsync, and a memset recorded into a graph has produced wrong results on
+replays after the first on MI355X (a wrong token then indexes past the embedding table).
 """
 
 from __future__ import annotations
@@ -101,7 +104,10 @@ class AicasGraphDecodeRunner:
         if self.static_logits is None:
             self.static_logits = torch.empty_like(logits)
         self.static_logits.copy_(logits)
-        self.static_next_token.copy_(logits[:, -1, :].argmax(dim=-1, keepdim=True))
+
+    def _pick(self) -> None:
+        """Greedy choice from the step's logits (outside any graph)."""
+        torch.argmax(self.static_logits[:, -1, :], dim=-1, keepdim=True, out=self.static_next_token)
 
     def _set_static(self, on: bool) -> None:
         for layer in self.cache.layers:
@@ -131,6 +137,7 @@ class AicasGraphDecodeRunner:
             with torch.cuda.stream(side):
                 for _ in range(3):
                     self._run_step()
+                    self._pick()
             torch.cuda.current_stream().wait_stream(side)
             torch.cuda.synchronize()
             # the warm-up steps appended rows past the prefix and bumped the lengths: take the lengths back
@@ -149,14 +156,16 @@ class AicasGraphDecodeRunner:
         return True
 
     def replay(self) -> torch.Tensor:
-        """Run the captured step for the staged inputs: every layer appends the step's K/V and bumps its lengths
-        on the device. Returns the static ``[B, 1]`` next-token buffer (overwritten by the next replay)."""
+        """Run the captured step for the staged inputs (every layer appends the step's K/V and bumps its lengths
+        on the device), then take the greedy token from its logits. Returns the static ``[B, 1]`` next-token
+        buffer (overwritten by the next replay)."""
         if not self.is_captured:
             raise RuntimeError("nothing captured: call maybe_capture first")
         first = self.cache.layers[0]
         if max(first.host_lens) + 1 > first.view.max_tokens:
             raise RuntimeError(f"KV cache capacity exceeded: {max(first.host_lens)} + 1 > {first.view.max_tokens}")
         self.graph.replay()
+        self._pick()
         for layer in self.cache.layers:
             layer.host_lens = [L + 1 for L in layer.host_lens]
         return self.static_next_token

@@ -17,6 +17,11 @@ The other seeded configurations of aicas_amd.workloads run with --config:
   c4  B=64, 28 layers, ragged lengths ~ U{512..4096}, one step, repeated;
   c5  B=32, 1 layer, ragged lengths ~ U{256..8192}, paged fp8 (16-token pages, permuted block table, 1%
       outliers), one step, repeated.
+and, reported separately from the headline, --config model: a whole decode step of a Qwen3-VL-2B-shaped text
+decoder (28 layers, hidden 2048, 16/8 heads, head_dim 128, MLP 6144, vocabulary 151936; random bf16 weights)
+per generated token at batch 1 after a --prompt-len prefill, three ways: HF eager (DynamicCache + SDPA, the
+reference's default decode), eager with every layer's attention as one fused launch (install_fused_decode +
+AicasDecodeCache), and the step captured once as a HIP graph and replayed (AicasGraphDecodeRunner).
 A one-layer configuration whose cache is smaller than 512 MB keeps several instances of it (>= 4, > 512 MB in
 all) and steps through them in turn, so that the 256 MB MALL cannot serve the reads; its step time is the
 per-layer time. One-step configurations repeat their step with the positions held, so every repeat appends
@@ -53,7 +58,9 @@ MALL_BYTES = 256 << 20
 def parse_args(argv=None):
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--config", choices=("c1", "c2", "c3", "c4", "c5"), default="c2")
+    p.add_argument("--config", choices=("c1", "c2", "c3", "c4", "c5", "model"), default="c2",
+                   help="model: the whole text-decoder step per generated token (reported separately)")
+    p.add_argument("--prompt-len", type=int, default=1024, help="model: cached tokens before the timed steps")
     p.add_argument("--steps", type=int, default=0, help="timed steps (0: the configuration's default)")
     p.add_argument("--warmup", type=int, default=16)
     p.add_argument("--mode", choices=("graph", "eager"), default="graph")
@@ -120,8 +127,139 @@ def percentile(xs, p):
     return ys[lo] + (ys[hi] - ys[lo]) * (k - lo)
 
 
+def model_step(args) -> int:
+    """--config model: µs per generated token for the whole text-decoder step (see the module docstring)."""
+    import copy
+
+    import torch
+    from transformers.cache_utils import DynamicCache
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLTextConfig
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import Qwen3VLTextModel
+
+    import aicas_amd.fused_attention as fa
+    from aicas_amd.graph_runner import AicasGraphDecodeRunner
+    from aicas_amd.kv_cache import AicasDecodeCache
+
+    t_start = time.perf_counter()
+
+    def progress(what):
+        print(f"[model +{time.perf_counter() - t_start:.1f}s] {what}", file=sys.stderr, flush=True)
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    K, W, P = args.steps or 64, max(args.warmup, 2), args.prompt_len
+    cfg = Qwen3VLTextConfig(vocab_size=151936, hidden_size=2048, intermediate_size=6144, num_hidden_layers=28,
+                            num_attention_heads=16, num_key_value_heads=8, head_dim=128, rms_norm_eps=1e-6,
+                            rope_theta=5e6, max_position_embeddings=P + K + W + 64)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(0)
+    progress("building the model")
+    default_dtype = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(dev):
+            model = Qwen3VLTextModel(cfg).eval()
+            lm_head = torch.nn.Linear(2048, 151936, bias=False)
+    finally:
+        torch.set_default_dtype(default_dtype)
+    progress("model built")
+    gen = torch.Generator(device=dev).manual_seed(1)
+    prompt = torch.randint(0, 151936, (1, P), generator=gen, device=dev)
+    with torch.no_grad():
+        prefix = DynamicCache(config=cfg)
+        h = model(input_ids=prompt, past_key_values=prefix, use_cache=True).last_hidden_state
+        tok0 = lm_head(h[:, -1:, :]).argmax(-1)
+    torch.cuda.synchronize()
+    progress(f"prefill of {P} tokens done")
+    cap = P + K + W + 8
+
+    def timed(step, n):
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / n
+
+    results = {}
+    with torch.no_grad():
+        # HF eager: DynamicCache (torch.cat per layer and step) + SDPA
+        cache = copy.deepcopy(prefix)
+        state = {"tok": tok0.clone(), "pos": torch.full((1, 1), P, dtype=torch.long, device=dev)}
+
+        def hf_step():
+            hh = model(input_ids=state["tok"], past_key_values=cache, use_cache=True,
+                       position_ids=state["pos"]).last_hidden_state
+            state["tok"] = lm_head(hh[:, -1:, :]).argmax(-1)
+            state["pos"] = state["pos"] + 1
+
+        for _ in range(W):
+            hf_step()
+        results["hf_eager_us"] = timed(hf_step, K)
+        progress(f"HF eager: {results['hf_eager_us']:.1f} us/token")
+        del cache
+        # eager, attention fused (q/k norm + rotary + append + attend in one launch per layer)
+        acache = AicasDecodeCache(num_layers=28, max_cache_len=cap)
+        for src, dst in zip(prefix.layers, acache.layers):
+            dst.load_prefix(src.keys, src.values)
+        fa.install_fused_decode(model)
+        state = {"tok": tok0.clone(), "pos": torch.full((1, 1), P, dtype=torch.long, device=dev)}
+
+        def fused_step():
+            hh = model(input_ids=state["tok"], past_key_values=acache, use_cache=True,
+                       position_ids=state["pos"]).last_hidden_state
+            state["tok"] = lm_head(hh[:, -1:, :]).argmax(-1)
+            state["pos"] = state["pos"] + 1
+
+        for _ in range(W):
+            fused_step()
+        results["fused_eager_us"] = timed(fused_step, K)
+        progress(f"fused eager: {results['fused_eager_us']:.1f} us/token")
+        del acache
+        # the step captured once as a HIP graph
+        runner = AicasGraphDecodeRunner(model, lm_head, max_cache_len=cap)
+        pos = torch.full((1, 1), P, dtype=torch.long, device=dev)
+        assert runner.maybe_capture(prefix, P, tok0, pos)
+        progress("graph captured")
+        state = {"pos": pos}
+
+        def graph_step():
+            runner.prepare_step(runner.static_next_token, state["pos"])
+            runner.replay()
+            state["pos"] = state["pos"] + 1
+
+        for _ in range(W):
+            graph_step()
+        results["graph_us"] = timed(graph_step, K)
+        progress(f"graph: {results['graph_us']:.1f} us/token")
+        runner.release()
+        fa.uninstall_fused_decode(model)
+    out = {
+        "metric": "us per generated token, whole Qwen3-VL-2B text-decoder decode step (reported beside the "
+                  "headline, not the headline)",
+        "value": round(results["graph_us"], 1),
+        "unit": "us/token",
+        "n_gpus": 1, "steps": K, "warmup": W, "ms_per_step": round(results["graph_us"] / 1e3, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random bf16 weights and prompt)",
+        "config": {"workload": f"qwen3vl-2b text decoder step, B=1, {P} cached tokens, 28 layers, vocab 151936",
+                   "batch": 1, "cached_before": P},
+        "hf_eager_us_per_token": round(results["hf_eager_us"], 1),
+        "fused_eager_us_per_token": round(results["fused_eager_us"], 1),
+        "graph_us_per_token": round(results["graph_us"], 1),
+        "tokens_per_s_graph": round(1e6 / results["graph_us"], 1),
+        "speedup_graph_vs_hf_eager": round(results["hf_eager_us"] / results["graph_us"], 2),
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
+    if args.config == "model" and args.gpus == 1:
+        return model_step(args)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: each GPU serves its own "
               "sequences (or kv heads), so the step does not shard across GPUs here.", file=sys.stderr)

@@ -82,6 +82,47 @@ def test_graph_runner_matches_eager_decode(dev, B, kv_dtype, page_size):
     assert lens == [P + steps] * B
 
 
+def test_graph_runner_back_to_back_replays(dev):
+    """Replays issued back to back with the token fed back on the device (no host synchronisation in between,
+    as a serving loop runs them), then checked against HF's eager decode fed the same tokens."""
+    from transformers.cache_utils import DynamicCache
+
+    from aicas_amd.graph_runner import AicasGraphDecodeRunner
+    import aicas_amd.fused_attention as fa
+
+    vocab, P, steps = 151936, 17, 24
+    cfg, model, lm_head = _model(dev, vocab)
+    prompt = torch.randint(0, vocab, (1, P), generator=torch.Generator().manual_seed(9)).to(dev)
+    with torch.no_grad():
+        prefix = DynamicCache(config=cfg)
+        h = model(input_ids=prompt, past_key_values=prefix, use_cache=True).last_hidden_state
+        tok = lm_head(h[:, -1:, :]).argmax(-1)
+        eager_cache = copy.deepcopy(prefix)
+        runner = AicasGraphDecodeRunner(model, lm_head, max_cache_len=P + steps + 2)
+        pos = torch.full((1, 1), P, dtype=torch.long, device=dev)
+        assert runner.maybe_capture(prefix, P, tok, pos)
+        fed = torch.empty((steps, 1, 1), dtype=torch.long, device=dev)
+        logits = torch.empty((steps, 1, 1, vocab), dtype=torch.bfloat16, device=dev)
+        fed[0].copy_(tok)
+        try:
+            for s in range(steps):
+                runner.prepare_step(fed[s], pos + s)
+                nxt = runner.replay()
+                logits[s].copy_(runner.static_logits)
+                if s + 1 < steps:
+                    fed[s + 1].copy_(nxt)
+            torch.cuda.synchronize()
+        finally:
+            runner.release()
+            fa.uninstall_fused_decode(model)
+        assert int(fed.max()) < vocab and int(fed.min()) >= 0
+        for s in range(steps):
+            h = model(input_ids=fed[s], past_key_values=eager_cache, use_cache=True, position_ids=pos + s).last_hidden_state
+            want = lm_head(h[:, -1:, :]).float()
+            err = float((logits[s].float() - want).norm() / want.norm())
+            assert err < 3e-2, (s, err)
+
+
 def test_graph_runner_rejects_mismatched_shapes(dev):
     from transformers.cache_utils import DynamicCache
 
