@@ -18,7 +18,7 @@ import torch  # noqa: F401  (must precede the library load, see above)
 LIB_NAME = "libaicas_decode.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_BF16 = 0
 DTYPE_FP16 = 1
@@ -33,6 +33,7 @@ ERR_LAUNCH = 4
 STATUS_LEN_CLAMPED = 1
 STATUS_BLOCK_OUT_OF_RANGE = 2
 STATUS_APPEND_OVERFLOW = 4
+STATUS_OUT_OF_BLOCKS = 8
 
 # Entry points declared in include/aicas_decode.h, in declaration order.
 EXPORTED_SYMBOLS = (
@@ -41,6 +42,9 @@ EXPORTED_SYMBOLS = (
     "aicas_decode_attention",
     "aicas_decode_attention_append",
     "aicas_decode_attention_append_qk",
+    "aicas_block_pool_init",
+    "aicas_block_alloc",
+    "aicas_block_free",
     "aicas_last_error",
     "aicas_abi_version",
 )
@@ -73,6 +77,12 @@ class KVCacheDesc(ctypes.Structure):
         ("page_size", ctypes.c_int32),
         ("kv_dtype", ctypes.c_int32),
     ]
+
+
+class BlockPoolDesc(ctypes.Structure):
+    """aicas_block_pool_t (include/aicas_decode.h)."""
+
+    _fields_ = [("free_blocks", ctypes.c_void_p), ("free_count", ctypes.c_void_p), ("num_blocks", ctypes.c_int32)]
 
 
 class QKPrologueDesc(ctypes.Structure):
@@ -142,6 +152,12 @@ def _bind(handle: ctypes.CDLL) -> ctypes.CDLL:
     handle.aicas_decode_attention_append_qk.restype = ctypes.c_int
     handle.aicas_decode_attention_append_qk.argtypes = [ctypes.POINTER(KVCacheDesc), ctypes.POINTER(QKPrologueDesc)] + \
         handle.aicas_decode_attention_append.argtypes[1:]
+    handle.aicas_block_pool_init.restype = ctypes.c_int
+    handle.aicas_block_pool_init.argtypes = [ctypes.POINTER(BlockPoolDesc), _P]
+    handle.aicas_block_alloc.restype = ctypes.c_int
+    handle.aicas_block_alloc.argtypes = [ctypes.POINTER(BlockPoolDesc), _P, _I64, _I32, _P, _I32, _I32, _I32, _P, _P]
+    handle.aicas_block_free.restype = ctypes.c_int
+    handle.aicas_block_free.argtypes = [ctypes.POINTER(BlockPoolDesc), _P, _I64, _I32, _P, _P, _I32, _P, _P]
     return handle
 
 

@@ -9,6 +9,7 @@
 #include <algorithm>
 
 #include "aicas_decode.h"
+#include "block_pool.hpp"
 #include "decode_attn.hpp"
 #include "kv_append.hpp"
 
@@ -498,6 +499,79 @@ int aicas_decode_attention_append_qk(const aicas_kv_cache_t* cache, const aicas_
                        v_stride_b, v_stride_h, out, out_stride_b, out_stride_h, positions, seq_lens_out, min_len,
                        max_seq_len, batch, num_q_heads, num_kv_heads, head_dim, sm_scale, tokens_per_split, workspace,
                        workspace_bytes, status, stream);
+}
+
+namespace {
+int check_pool(const aicas_block_pool_t* pool) {
+  if (!pool || !pool->free_blocks || !pool->free_count) return fail(AICAS_ERR_INVALID, "block pool pointers must be non-NULL");
+  if (pool->num_blocks <= 0) return fail(AICAS_ERR_INVALID, "num_blocks must be positive");
+  return 0;
+}
+int check_table(const int32_t* table, int64_t stride, int32_t width) {
+  if (!table) return fail(AICAS_ERR_INVALID, "block_table must be non-NULL");
+  if (width <= 0 || stride < width) return fail(AICAS_ERR_INVALID, "block table width must be positive and <= its row stride");
+  return 0;
+}
+}  // namespace
+
+int aicas_block_pool_init(const aicas_block_pool_t* pool, hipStream_t stream) {
+  int rc = check_pool(pool);
+  if (rc) return rc;
+  const int blocks = static_cast<int>(std::min<int64_t>(ceil_div(pool->num_blocks, aicas::kPoolThreads), 1024));
+  hipLaunchKernelGGL(aicas::block_pool_init_kernel, dim3(blocks), dim3(aicas::kPoolThreads), 0, stream,
+                     pool->free_blocks, pool->free_count, pool->num_blocks);
+  return check_launch("aicas_block_pool_init");
+}
+
+int aicas_block_alloc(const aicas_block_pool_t* pool, int32_t* block_table, int64_t block_table_stride,
+                      int32_t table_width, const int32_t* positions, int32_t n_new, int32_t batch, int32_t page_size,
+                      int32_t* status, hipStream_t stream) {
+  int rc = check_pool(pool);
+  if (!rc) rc = check_table(block_table, block_table_stride, table_width);
+  if (rc) return rc;
+  if (!positions) return fail(AICAS_ERR_INVALID, "positions must be non-NULL");
+  if (n_new < 1) return fail(AICAS_ERR_INVALID, "n_new must be >= 1");
+  if (batch < 0) return fail(AICAS_ERR_INVALID, "batch must be >= 0");
+  if (!is_pow2(page_size)) return fail(AICAS_ERR_INVALID, "page_size must be a power of two");
+  if (batch == 0) return ok();
+  aicas::BlockPoolParams p{};
+  p.free_blocks = pool->free_blocks;
+  p.free_count = pool->free_count;
+  p.num_blocks = pool->num_blocks;
+  p.table = block_table;
+  p.stride = block_table_stride;
+  p.width = table_width;
+  p.batch = batch;
+  p.positions = positions;
+  p.n_new = n_new;
+  p.page_shift = ilog2(page_size);
+  p.status = status;
+  hipLaunchKernelGGL(aicas::block_alloc_kernel, dim3(1), dim3(aicas::kPoolThreads), 0, stream, p);
+  return check_launch("aicas_block_alloc");
+}
+
+int aicas_block_free(const aicas_block_pool_t* pool, int32_t* block_table, int64_t block_table_stride,
+                     int32_t table_width, const int32_t* release, int32_t* seq_lens, int32_t batch, int32_t* status,
+                     hipStream_t stream) {
+  int rc = check_pool(pool);
+  if (!rc) rc = check_table(block_table, block_table_stride, table_width);
+  if (rc) return rc;
+  if (!release) return fail(AICAS_ERR_INVALID, "release must be non-NULL");
+  if (batch < 0) return fail(AICAS_ERR_INVALID, "batch must be >= 0");
+  if (batch == 0) return ok();
+  aicas::BlockPoolParams p{};
+  p.free_blocks = pool->free_blocks;
+  p.free_count = pool->free_count;
+  p.num_blocks = pool->num_blocks;
+  p.table = block_table;
+  p.stride = block_table_stride;
+  p.width = table_width;
+  p.batch = batch;
+  p.release = release;
+  p.seq_lens = seq_lens;
+  p.status = status;
+  hipLaunchKernelGGL(aicas::block_free_kernel, dim3(1), dim3(aicas::kPoolThreads), 0, stream, p);
+  return check_launch("aicas_block_free");
 }
 
 }  // extern "C"

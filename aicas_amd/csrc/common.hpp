@@ -15,6 +15,7 @@ enum StatusBits : int32_t {
   kStatusLenClamped = 1,      // seq_len exceeded what the cache (or the block table) can hold
   kStatusBlockOutOfRange = 2, // a block-table entry was outside [0, num_blocks)
   kStatusAppendOverflow = 4,  // an append position was outside the cache; the row was dropped
+  kStatusOutOfBlocks = 8,     // the block pool ran out: a page was left without a block
 };
 
 constexpr int kWave = 64;

@@ -27,14 +27,14 @@ from .kv_cache import AicasDecodeCache
 
 class AicasGraphDecodeRunner:
     def __init__(self, language_model, lm_head, max_cache_len: int, batch_size: int = 1,
-                 kv_dtype: torch.dtype | None = None, page_size: int | None = None):
+                 kv_dtype: torch.dtype | None = None, page_size: int | None = None, block_pool: bool = False):
         self.language_model = language_model
         self.lm_head = lm_head
         self.max_cache_len = int(max_cache_len)
         self.batch_size = int(batch_size)
         self.device = lm_head.weight.device
         self.cache = AicasDecodeCache(num_layers=len(language_model.layers), max_cache_len=self.max_cache_len,
-                                      kv_dtype=kv_dtype, page_size=page_size)
+                                      kv_dtype=kv_dtype, page_size=page_size, block_pool=block_pool)
         B = self.batch_size
         self.static_input_ids = torch.zeros((B, 1), dtype=torch.long, device=self.device)
         self.static_position_ids = torch.zeros((3, B, 1), dtype=torch.long, device=self.device)

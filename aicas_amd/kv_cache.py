@@ -48,8 +48,11 @@ class AicasKVCacheLayer(CacheLayerMixin):
         page_size: int | None = None,
         num_blocks: int | None = None,
         block_table: torch.Tensor | None = None,
+        block_pool: bool = False,
     ):
         super().__init__()
+        if block_pool and (page_size is None or block_table is not None):
+            raise ValueError("block_pool needs a paged cache whose block table it owns (page_size, no block_table)")
         if kv_dtype not in (None, torch.bfloat16, torch.float16, ops.FP8_DTYPE):
             raise ValueError(f"unsupported kv_dtype {kv_dtype}")
         if page_size is not None and (page_size <= 0 or page_size & (page_size - 1)):
@@ -59,6 +62,8 @@ class AicasKVCacheLayer(CacheLayerMixin):
         self.page_size = page_size
         self.num_blocks = num_blocks
         self._given_block_table = block_table
+        self.use_block_pool = bool(block_pool)
+        self.pool: ops.BlockPool | None = None  # device block allocator (block_pool=True)
         self.k_scale = None
         self.v_scale = None
         self.block_table = None
@@ -92,6 +97,11 @@ class AicasKVCacheLayer(CacheLayerMixin):
                 if bt.shape[0] != B:
                     raise ValueError("block_table must have one row per sequence")
                 nblocks = self.num_blocks or int(bt.max().item()) + 1
+            elif self.use_block_pool:
+                # pages get blocks from the device pool as appends reach them
+                nblocks = self.num_blocks or B * per_seq
+                bt = torch.full((B, per_seq), -1, dtype=torch.int32, device=dev)
+                self.pool = ops.BlockPool(nblocks, dev)
             else:
                 nblocks = self.num_blocks or B * per_seq
                 if nblocks < B * per_seq:
@@ -119,9 +129,15 @@ class AicasKVCacheLayer(CacheLayerMixin):
             raise RuntimeError(
                 f"KV cache capacity exceeded: {max(self.host_lens)} + {n} > {self.view.max_tokens} tokens"
             )
+        self._reserve(self.seq_lens, n)
         ops.kv_append(self.view, key_states, value_states, self.seq_lens, self.seq_lens)
         self.host_lens = [L + n for L in self.host_lens]
         return self._result(key_states, value_states, n, was_empty)
+
+    def _reserve(self, positions: torch.Tensor, n: int) -> None:
+        """With a block pool: blocks for the pages an append of n tokens at positions will touch."""
+        if self.pool is not None:
+            self.pool.alloc(self.block_table, positions, n, self.page_size)
 
     def get_mask_sizes(self, query_length: int) -> tuple[int, int]:
         return self.get_seq_length() + query_length, 0
@@ -136,6 +152,9 @@ class AicasKVCacheLayer(CacheLayerMixin):
 
     def reset(self) -> None:
         if self.is_initialized:
+            if self.pool is not None:  # every sequence's blocks back to the pool (rows -1, lengths 0)
+                self.pool.free(self.block_table, torch.ones(self.batch, dtype=torch.int32, device=self.device),
+                               self.seq_lens)
             self.seq_lens.zero_()
             self.host_lens = [0] * self.batch
 
@@ -159,6 +178,8 @@ class AicasKVCacheLayer(CacheLayerMixin):
         if L > self.view.max_tokens:
             raise RuntimeError("prefix longer than the cache capacity")
         zeros = torch.zeros(B, dtype=torch.int32, device=self.device)
+        if L > 0:
+            self._reserve(zeros, L)
         ops.kv_append(self.view, keys, values, zeros)
         self.seq_lens.copy_(torch.tensor(lens, dtype=torch.int32), non_blocking=False)
         self.host_lens = lens
@@ -171,6 +192,7 @@ class AicasKVCacheLayer(CacheLayerMixin):
         embedding) inside the launch as the model would."""
         if not self.is_initialized:
             raise RuntimeError("the cache layer is empty: prefill through update() first")
+        self._reserve(self.seq_lens, 1)
         if self.static_bound is not None:
             # graph mode: nothing host-side may depend on the step (the runner checks capacity and advances
             # host_lens per replay); a token with no slot left is dropped and reported by the kernel
@@ -207,7 +229,10 @@ class AicasKVCacheLayer(CacheLayerMixin):
 
 
 class AicasDecodeCache(Cache):
-    """One :class:`AicasKVCacheLayer` per decoder layer; pass as ``past_key_values`` to ``generate``."""
+    """One :class:`AicasKVCacheLayer` per decoder layer; pass as ``past_key_values`` to ``generate``.
+    ``block_pool=True`` (paged caches) hands out pages from a device block pool as appends reach them, instead
+    of a fixed identity block table; ``num_blocks`` sizes each layer's pool (default: enough for every sequence
+    at full capacity)."""
 
     def __init__(
         self,
@@ -216,6 +241,8 @@ class AicasDecodeCache(Cache):
         kv_dtype: torch.dtype | None = None,
         page_size: int | None = None,
         config=None,
+        block_pool: bool = False,
+        num_blocks: int | None = None,
     ):
         if num_layers is None:
             if config is None:
@@ -223,7 +250,8 @@ class AicasDecodeCache(Cache):
             text_config = config.get_text_config() if hasattr(config, "get_text_config") else config
             num_layers = text_config.num_hidden_layers
         layers = [
-            AicasKVCacheLayer(max_cache_len=max_cache_len, kv_dtype=kv_dtype, page_size=page_size)
+            AicasKVCacheLayer(max_cache_len=max_cache_len, kv_dtype=kv_dtype, page_size=page_size,
+                              num_blocks=num_blocks, block_pool=block_pool)
             for _ in range(num_layers)
         ]
         super().__init__(layers=layers)

@@ -189,6 +189,68 @@ def kv_append(
     )
 
 
+class BlockPool:
+    """Free block ids of a paged cache's pool, kept on the device (``aicas_block_pool_t``): ``alloc`` gives the
+    pages an append is about to touch a block, ``free`` takes a finished sequence's blocks back — both kernels
+    on the current stream, so a decode step that needs a new page stays free of host synchronisation (and can be
+    captured in a HIP graph). Replaces the reference's Python page table (new KV cache/evaluation_wrapper.py:141-190).
+    """
+
+    def __init__(self, num_blocks: int, device: torch.device | str = "cuda"):
+        if num_blocks <= 0:
+            raise AicasError(_lib.ERR_INVALID, "num_blocks must be positive")
+        self.num_blocks = int(num_blocks)
+        self.device = torch.device(device)
+        self.free_blocks = torch.empty(self.num_blocks, dtype=torch.int32, device=self.device)
+        self.free_count = torch.empty(1, dtype=torch.int32, device=self.device)
+        _require_gpu(self.free_blocks)
+        self.reset()
+
+    def desc(self) -> _lib.BlockPoolDesc:
+        return _lib.BlockPoolDesc(self.free_blocks.data_ptr(), self.free_count.data_ptr(), self.num_blocks)
+
+    def reset(self) -> None:
+        """Every block free again; pops hand out 0, 1, 2, ..."""
+        check(_lib.lib().aicas_block_pool_init(ctypes.byref(self.desc()), _stream(self.device)))
+
+    @staticmethod
+    def _check_table(block_table: torch.Tensor) -> None:
+        if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.stride(1) != 1:
+            raise AicasError(_lib.ERR_INVALID, "block_table must be an int32 [batch, width] tensor with unit column stride")
+
+    def alloc(self, block_table: torch.Tensor, positions: torch.Tensor, n_new: int, page_size: int,
+              status: torch.Tensor | None = None) -> None:
+        """Give every page that an append of ``n_new`` tokens at ``positions[b]`` touches a block where
+        ``block_table`` holds a negative entry (in sequence order, each sequence's pages in page order)."""
+        self._check_table(block_table)
+        B = block_table.shape[0]
+        if positions.dtype != torch.int32 or positions.numel() < B or not positions.is_contiguous():
+            raise AicasError(_lib.ERR_INVALID, "positions must be a contiguous int32 tensor with one entry per sequence")
+        _require_gpu(self.free_blocks, block_table, positions, status)
+        check(_lib.lib().aicas_block_alloc(
+            ctypes.byref(self.desc()), block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
+            positions.data_ptr(), int(n_new), B, int(page_size), _ptr(status), _stream(self.device)))
+
+    def free(self, block_table: torch.Tensor, release: torch.Tensor, seq_lens: torch.Tensor | None = None,
+             status: torch.Tensor | None = None) -> None:
+        """Return the blocks of every sequence with ``release[b] != 0`` (int32) to the pool; their rows become -1
+        and, if given, their ``seq_lens`` 0."""
+        self._check_table(block_table)
+        B = block_table.shape[0]
+        if release.dtype != torch.int32 or release.numel() < B or not release.is_contiguous():
+            raise AicasError(_lib.ERR_INVALID, "release must be a contiguous int32 tensor with one entry per sequence")
+        if seq_lens is not None and (seq_lens.dtype != torch.int32 or not seq_lens.is_contiguous()):
+            raise AicasError(_lib.ERR_INVALID, "seq_lens must be a contiguous int32 tensor")
+        _require_gpu(self.free_blocks, block_table, release, seq_lens, status)
+        check(_lib.lib().aicas_block_free(
+            ctypes.byref(self.desc()), block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
+            release.data_ptr(), _ptr(seq_lens), B, _ptr(status), _stream(self.device)))
+
+    def available(self) -> int:
+        """Free blocks left (reads the device count: synchronises with the stream)."""
+        return int(self.free_count.item())
+
+
 @dataclass(frozen=True)
 class DecodePlan:
     tokens_per_split: int

@@ -67,6 +67,9 @@ def parse_args(argv=None):
     p.add_argument("--path", choices=("fused", "separate"), default="fused",
                    help="fused: one launch per layer appends and attends; separate: append kernel + decode kernel")
     p.add_argument("--compare-paths", type=int, default=1, help="also time the other path (reported, not the value)")
+    p.add_argument("--compare-pool", type=int, default=1,
+                   help="paged configurations: also time the fused path with a device page allocation before "
+                        "each launch (aicas_block_alloc; reported, not the value)")
     p.add_argument("--compare-qk", type=int, default=1,
                    help="also time the fused path with the q/k RMSNorm + rotary prologue (reported, not the value)")
     p.add_argument("--tokens-per-split", type=int, default=0, help="0 = the library's plan")
@@ -354,7 +357,10 @@ def main(argv=None) -> int:
     def step(s, path, kernel_events=None):
         """One decode step: for every layer append this step's K/V row and attend."""
         for i in range(NL):
-            if path in ("fused", "fused_qk"):
+            if path == "fused_pool":
+                # the device block pool gives the page the append will write a block (when it has none yet)
+                pools[i].alloc(views[i].block_table, shared_lens, 1, page)
+            if path in ("fused", "fused_qk", "fused_pool"):
                 qk = None
                 if path == "fused_qk":
                     qn_w, kn_w, cos_all, sin_all, q_prep = qk_all
@@ -444,6 +450,14 @@ def main(argv=None) -> int:
         graphs_other = capture(other) if args.mode == "graph" else None
         other_us = timed(other, graphs_other)[0] * 1e3 / K * layer_weight
         del graphs_other
+    pool_us = None
+    if w.paged and args.compare_pool:
+        # one pool per cache instance, every block free; the tables were filled at set-up, so a step's
+        # allocation scans its pages and pops nothing (a page is new only every page_size steps)
+        pools = [ops.BlockPool(views[i].k.shape[0], dev) for i in range(NL)]
+        graphs_pool = capture("fused_pool") if args.mode == "graph" else None
+        pool_us = timed("fused_pool", graphs_pool)[0] * 1e3 / K * layer_weight
+        del graphs_pool
     qk_us = None
     if args.compare_qk:
         graphs_qk = capture("fused_qk") if args.mode == "graph" else None
@@ -651,6 +665,7 @@ def main(argv=None) -> int:
         "wall_ms": round(wall_ms, 3),
         f"{other}_path_us_per_step": None if other_us is None else round(other_us, 2),
         "fused_qk_path_us_per_step": None if qk_us is None else round(qk_us, 2),
+        "fused_with_block_pool_us_per_step": None if pool_us is None else round(pool_us, 2),
         "roofline": {
             "bound": "hbm",
             "kernel": f"decode_attn_kernel<bf16,{kv_name},D=128,G=2,{'paged' if w.paged else 'contiguous'},"

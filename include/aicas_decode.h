@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define AICAS_ABI_VERSION 4
+#define AICAS_ABI_VERSION 5
 
 /* Element types. */
 #define AICAS_DTYPE_BF16 0
@@ -53,6 +53,7 @@ extern "C" {
 #define AICAS_STATUS_LEN_CLAMPED 1
 #define AICAS_STATUS_BLOCK_OUT_OF_RANGE 2
 #define AICAS_STATUS_APPEND_OVERFLOW 4
+#define AICAS_STATUS_OUT_OF_BLOCKS 8
 
 /*
  * A KV cache. Two layouts share one description:
@@ -202,6 +203,43 @@ int aicas_decode_attention_append_qk(const aicas_kv_cache_t* cache, const aicas_
 
 /* Message describing the last failure on the calling thread ("" if none). */
 const char* aicas_last_error(void);
+
+/*
+ * Device block pool for paged caches: free block ids kept as a stack in device memory (free_blocks[0 ..
+ * *free_count) are free, the top is the last), handed out to pages and taken back by kernels on the stream, so
+ * that a decode step that needs a new page still involves no host synchronisation. The table is the int32
+ * [batch, width] block table of aicas_kv_cache_t (-1: no block). Allocation and release run in sequence order
+ * (sequence b's pages in page order), so the resulting table is reproducible.
+ * Replaces: new KV cache/evaluation_wrapper.py:141-190 (the page table as a Python list of
+ * {"logical_page_id", "block_id"} dicts, grown by list.append as pages fill), :198-232 (its walk) and
+ * :502-521 (its reset).
+ */
+typedef struct aicas_block_pool {
+  int32_t* free_blocks; /* [num_blocks] device */
+  int32_t* free_count;  /* [1] device */
+  int32_t num_blocks;
+} aicas_block_pool_t;
+
+/* Every block free: pops then hand out 0, 1, 2, ... */
+int aicas_block_pool_init(const aicas_block_pool_t* pool, hipStream_t stream);
+
+/*
+ * Before appending n_new (>= 1) tokens at positions[b]: every page those tokens touch whose table entry is
+ * negative gets the next free block. Pages past the row's width set AICAS_STATUS_APPEND_OVERFLOW; when the pool
+ * runs out the entry stays -1 and AICAS_STATUS_OUT_OF_BLOCKS is set (the append then drops those rows).
+ */
+int aicas_block_alloc(const aicas_block_pool_t* pool, int32_t* block_table, int64_t block_table_stride,
+                      int32_t table_width, const int32_t* positions, int32_t n_new, int32_t batch, int32_t page_size,
+                      int32_t* status, hipStream_t stream);
+
+/*
+ * Every sequence with release[b] != 0 returns its blocks to the pool; its table row becomes -1 and, if seq_lens
+ * is not NULL, seq_lens[b] = 0. Ids outside [0, num_blocks), and blocks that would overfill the pool (released
+ * twice), are dropped and set AICAS_STATUS_BLOCK_OUT_OF_RANGE.
+ */
+int aicas_block_free(const aicas_block_pool_t* pool, int32_t* block_table, int64_t block_table_stride,
+                     int32_t table_width, const int32_t* release, int32_t* seq_lens, int32_t batch, int32_t* status,
+                     hipStream_t stream);
 
 /* AICAS_ABI_VERSION of the loaded library. */
 int32_t aicas_abi_version(void);

@@ -15,7 +15,8 @@ It restates, in torch on the CPU, the reference path of Frun1na/AICAS:
     transformers/models/qwen3_vl/modeling_qwen3_vl.py:171-193): fp32 softmax cast back to the query dtype
     before the P.V product;
   * the paged layout (block table of fixed-size pages, new KV cache/evaluation_wrapper.py:143-232) with fp8
-    e4m3 (OCP "e4m3fn") rows and one fp32 scale per (token, kv head) in place of the KIVI 2-bit codec.
+    e4m3 (OCP "e4m3fn") rows and one fp32 scale per (token, kv head) in place of the KIVI 2-bit codec, and the
+    growth of its page table one page at a time (block_alloc / block_free).
 
 The reference ships no golden vectors for this path, so each function here is pinned in
 tests/test_oracle.py against closed forms, brute force and library routines (see the test docstrings).
@@ -213,6 +214,65 @@ def paged_gather(pool: torch.Tensor, block_table: torch.Tensor, lens: list[int])
         seq = blocks.transpose(0, 1).reshape(pool.shape[1], nb * page, *pool.shape[3:])
         out.append(seq[:, :L])
     return out
+
+
+# ----------------------------------------------------------------------------------------- block pool
+def block_pool_init(num_blocks: int) -> tuple[list[int], int]:
+    """A pool with every block free, as a stack whose pops hand out 0, 1, 2, ...: (stack, count)."""
+    return [num_blocks - 1 - i for i in range(num_blocks)], num_blocks
+
+
+def block_alloc(stack: list[int], count: int, table: torch.Tensor, positions: list[int], n_new: int,
+                page_size: int) -> tuple[int, int]:
+    """Sequential page-table growth: in sequence order, every page that tokens [positions[b], positions[b] + n_new)
+    touch and whose entry is negative takes the block on top of the stack — the reference grows its page table
+    one page at a time in the same way, appending {"logical_page_id", "block_id"} with the next block id
+    (new KV cache/evaluation_wrapper.py:164-190). Pages past the row's width set status 4 (append overflow); an
+    empty stack leaves the entry at -1 and sets status 8 (out of blocks). Mutates ``table``; returns
+    (new count, status)."""
+    status = 0
+    width = table.shape[1]
+    for b in range(table.shape[0]):
+        pos = max(int(positions[b]), 0)
+        first, last = pos // page_size, (pos + n_new - 1) // page_size
+        if last >= width:
+            status |= 4
+            last = width - 1
+        for pg in range(first, last + 1):
+            if int(table[b, pg]) < 0:
+                if count > 0:
+                    count -= 1
+                    table[b, pg] = stack[count]
+                else:
+                    status |= 8
+    return count, status
+
+
+def block_free(stack: list[int], count: int, table: torch.Tensor, release: list[int], seq_lens: list[int] | None,
+               num_blocks: int) -> tuple[int, int]:
+    """In sequence order, every released sequence pushes its valid block ids (page order) back onto the stack,
+    its row becomes -1 and its length 0 (the reference's reset drops the whole list, new KV
+    cache/evaluation_wrapper.py:502-521). Ids outside
+    [0, num_blocks) and pushes past a full stack are dropped with status 2. Mutates ``stack``, ``table`` and
+    ``seq_lens``; returns (new count, status)."""
+    status = 0
+    for b in range(table.shape[0]):
+        if not release[b]:
+            continue
+        for pg in range(table.shape[1]):
+            e = int(table[b, pg])
+            if 0 <= e < num_blocks:
+                if count < num_blocks:
+                    stack[count] = e
+                    count += 1
+                else:
+                    status |= 2
+            elif e >= num_blocks:
+                status |= 2
+            table[b, pg] = -1
+        if seq_lens is not None:
+            seq_lens[b] = 0
+    return count, status
 
 
 def paged_scatter_rows(

@@ -43,12 +43,14 @@ def test_constants_match_header():
                         ("AICAS_ERR_UNSUPPORTED", _lib.ERR_UNSUPPORTED), ("AICAS_ERR_WORKSPACE", _lib.ERR_WORKSPACE),
                         ("AICAS_ERR_LAUNCH", _lib.ERR_LAUNCH), ("AICAS_STATUS_LEN_CLAMPED", _lib.STATUS_LEN_CLAMPED),
                         ("AICAS_STATUS_BLOCK_OUT_OF_RANGE", _lib.STATUS_BLOCK_OUT_OF_RANGE),
-                        ("AICAS_STATUS_APPEND_OVERFLOW", _lib.STATUS_APPEND_OVERFLOW)]:
+                        ("AICAS_STATUS_APPEND_OVERFLOW", _lib.STATUS_APPEND_OVERFLOW),
+                        ("AICAS_STATUS_OUT_OF_BLOCKS", _lib.STATUS_OUT_OF_BLOCKS)]:
         assert re.search(rf"#define {name} {value}\b", text), name
 
 
 @pytest.mark.parametrize("ctype, struct", [("aicas_kv_cache_t", _lib.KVCacheDesc),
-                                           ("aicas_qk_prologue_t", _lib.QKPrologueDesc)])
+                                           ("aicas_qk_prologue_t", _lib.QKPrologueDesc),
+                                           ("aicas_block_pool_t", _lib.BlockPoolDesc)])
 def test_descriptor_layouts_match_header(tmp_path, ctype, struct):
     """The ctypes mirrors of the ABI's structs have the C compiler's layout (sizeof and every offsetof)."""
     fields = [f[0] for f in struct._fields_]
@@ -220,3 +222,27 @@ def test_fused_qk_entry_argument_errors():
     pro.q_norm_weight = FAKE
     pro.eps = -1.0
     assert call(ctypes.byref(pro)) == _lib.ERR_INVALID and "eps" in _last_error()
+
+
+def test_block_pool_argument_errors():
+    """Every rejected argument returns before anything reaches the GPU."""
+    lib = _lib.lib()
+    pool = _lib.BlockPoolDesc(FAKE, FAKE + 4096, 16)
+
+    def alloc(p=pool, table=FAKE + 8192, stride=4, width=4, pos=FAKE + 12288, n_new=1, batch=2, page=16):
+        return lib.aicas_block_alloc(ctypes.byref(p) if p is not None else None, table, stride, width, pos, n_new,
+                                     batch, page, None, None)
+
+    assert alloc(p=None) == _lib.ERR_INVALID and "pool" in _last_error()
+    assert alloc(p=_lib.BlockPoolDesc(FAKE, FAKE + 4096, 0)) == _lib.ERR_INVALID and "num_blocks" in _last_error()
+    assert alloc(table=None) == _lib.ERR_INVALID and "block_table" in _last_error()
+    assert alloc(width=0) == _lib.ERR_INVALID and "width" in _last_error()
+    assert alloc(stride=2) == _lib.ERR_INVALID and "stride" in _last_error()
+    assert alloc(pos=None) == _lib.ERR_INVALID and "positions" in _last_error()
+    assert alloc(n_new=0) == _lib.ERR_INVALID and "n_new" in _last_error()
+    assert alloc(page=12) == _lib.ERR_INVALID and "power of two" in _last_error()
+    assert alloc(batch=-1) == _lib.ERR_INVALID and "batch" in _last_error()
+    assert alloc(batch=0) == 0  # nothing to do: no launch
+    assert lib.aicas_block_free(ctypes.byref(pool), FAKE + 8192, 4, 4, None, None, 2, None, None) == _lib.ERR_INVALID
+    assert "release" in _last_error()
+    assert lib.aicas_block_pool_init(None, None) == _lib.ERR_INVALID

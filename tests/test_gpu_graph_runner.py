@@ -33,8 +33,9 @@ def _model(dev, vocab):
     return cfg, model, lm_head
 
 
-@pytest.mark.parametrize("B, kv_dtype, page_size", [(1, None, None), (2, None, None), (2, torch.float8_e4m3fn, 16)])
-def test_graph_runner_matches_eager_decode(dev, B, kv_dtype, page_size):
+@pytest.mark.parametrize("B, kv_dtype, page_size, block_pool", [
+    (1, None, None, False), (2, None, None, False), (2, torch.float8_e4m3fn, 16, False), (2, None, 4, True)])
+def test_graph_runner_matches_eager_decode(dev, B, kv_dtype, page_size, block_pool):
     from transformers.cache_utils import DynamicCache
 
     from aicas_amd.graph_runner import AicasGraphDecodeRunner
@@ -52,7 +53,7 @@ def test_graph_runner_matches_eager_decode(dev, B, kv_dtype, page_size):
         eager_cache = copy.deepcopy(prefix)
 
         runner = AicasGraphDecodeRunner(model, lm_head, max_cache_len=P + steps + 3, batch_size=B,
-                                        kv_dtype=kv_dtype, page_size=page_size)
+                                        kv_dtype=kv_dtype, page_size=page_size, block_pool=block_pool)
         pos = torch.full((B, 1), P, dtype=torch.long, device=dev)
         assert runner.maybe_capture(prefix, P, tok, pos)
         assert runner.cache.get_seq_length() == P
@@ -80,6 +81,10 @@ def test_graph_runner_matches_eager_decode(dev, B, kv_dtype, page_size):
     assert runner.cache.get_seq_length() == P + steps
     lens = runner.cache.layers[0].seq_lens.cpu().tolist()
     assert lens == [P + steps] * B
+    if block_pool:  # pages were handed out inside the captured steps, one block per page reached
+        layer = runner.cache.layers[0]
+        reached = -(-(P + steps) // page_size)
+        assert layer.pool.available() == layer.pool.num_blocks - B * reached
 
 
 def test_graph_runner_back_to_back_replays(dev):
