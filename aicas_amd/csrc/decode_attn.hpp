@@ -116,74 +116,40 @@ __device__ __forceinline__ float load_agent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// The model's q/k preparation for one head row held by the R lanes of a row group, N elements per lane
-// (element d = li * N + i): RMSNorm over head_dim in fp32, rounded to the storage type DT and multiplied by the
-// weight (Qwen3VLTextRMSNorm.forward, transformers/models/qwen3_vl/modeling_qwen3_vl.py:391-404), then the
-// rotary embedding x * cos + rotate_half(x) * sin with both products and the sum rounded to DT
-// (apply_rotary_pos_emb and rotate_half, modeling_qwen3_vl.py:412-438 and :138-142). rotate_half pairs element
-// d with d +- D/2, which lies R/2 lanes away (or in the same lane when R == 1). The lane's slices of the
-// weight and of the cos/sin row come in registers (QKSlices, fetched with the kernel's first loads); `norm` and
-// `rope` say which parts apply (uniform). Every lane of the row group must take part.
-template <int N>
-struct QKSlices {
-  uint4 qw[N / 8];  // q_norm weight
-  uint4 kw[N / 8];  // k_norm weight
-  uint4 cs[N / 8];  // cos row
-  uint4 sn[N / 8];  // sin row
-};
-
-template <int DT, int D, int R, int N>
-__device__ __forceinline__ void qk_prologue(float (&x)[N], int li, const uint4 (&weight)[N / 8], bool norm,
-                                            const uint4 (&cos_s)[N / 8], const uint4 (&sin_s)[N / 8], bool rope,
-                                            float eps) {
-  static_assert(N % 8 == 0 && R * N == D, "a row is R lanes of N elements");
+// The model's q/k preparation for one pair of adjacent elements (d0, d0 + 1) of a head row whose D/2 pairs are
+// held by D/2 consecutive lanes of one wave (every lane of the row must take part): RMSNorm over head_dim in
+// fp32, rounded to the storage type DT and multiplied by the weight (Qwen3VLTextRMSNorm.forward,
+// transformers/models/qwen3_vl/modeling_qwen3_vl.py:391-404), then the rotary embedding x * cos + rotate_half(x)
+// * sin with both products and the sum rounded to DT (apply_rotary_pos_emb and rotate_half,
+// modeling_qwen3_vl.py:412-438 and :138-142). rotate_half pairs element d with d +- D/2: the same slot of the
+// lane D/4 away. `norm` may differ between rows; `rope` is the same for all.
+template <int DT, int D>
+__device__ __forceinline__ void qk_pair(float& x0, float& x1, int d0, uint32_t weight, bool norm, uint32_t cos2,
+                                        uint32_t sin2, bool rope, float eps) {
+  constexpr int P = D / 2;  // lanes per row
+  static_assert(P <= kWave && kWave % P == 0, "a row's pairs must fit one wave");
+  float ss = __fadd_rn(__fmul_rn(x0, x0), __fmul_rn(x1, x1));
+#pragma unroll
+  for (int off = P / 2; off >= 1; off >>= 1) ss = __fadd_rn(ss, __shfl_xor(ss, off));
   if (norm) {
-    float ss = 0.0f;
-#pragma unroll
-    for (int i = 0; i < N; ++i) ss = __fadd_rn(ss, __fmul_rn(x[i], x[i]));
-    ss = group_sum<R>(ss);
     const float r = rsqrtf(__fadd_rn(ss * (1.0f / D), eps));
-#pragma unroll
-    for (int c = 0; c < N / 8; ++c) {
-      const uint32_t wv[4] = {weight[c].x, weight[c].y, weight[c].z, weight[c].w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float w0, w1;
-        unpack2<DT>(wv[j], w0, w1);
-        const int i = 8 * c + 2 * j;
-        x[i] = round_to<DT>(__fmul_rn(w0, round_to<DT>(__fmul_rn(x[i], r))));
-        x[i + 1] = round_to<DT>(__fmul_rn(w1, round_to<DT>(__fmul_rn(x[i + 1], r))));
-      }
-    }
+    float w0, w1;
+    unpack2<DT>(weight, w0, w1);
+    x0 = round_to<DT>(__fmul_rn(w0, round_to<DT>(__fmul_rn(x0, r))));
+    x1 = round_to<DT>(__fmul_rn(w1, round_to<DT>(__fmul_rn(x1, r))));
   }
   if (rope) {
-    float partner[N];
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      if constexpr (R >= 2) {
-        partner[i] = __shfl_xor(x[i], R / 2);
-      } else {
-        partner[i] = x[(i + N / 2) % N];
-      }
+    float p0 = __shfl_xor(x0, P / 2);
+    float p1 = __shfl_xor(x1, P / 2);
+    if (d0 < D / 2) {
+      p0 = -p0;
+      p1 = -p1;
     }
-#pragma unroll
-    for (int c = 0; c < N / 8; ++c) {
-      const uint32_t cv[4] = {cos_s[c].x, cos_s[c].y, cos_s[c].z, cos_s[c].w};
-      const uint32_t sv[4] = {sin_s[c].x, sin_s[c].y, sin_s[c].z, sin_s[c].w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float cs[2], sn[2];
-        unpack2<DT>(cv[j], cs[0], cs[1]);
-        unpack2<DT>(sv[j], sn[0], sn[1]);
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const int i = 8 * c + 2 * j + e;
-          const int d = li * N + i;
-          const float rot = d < D / 2 ? -partner[i] : partner[i];
-          x[i] = round_to<DT>(__fadd_rn(round_to<DT>(__fmul_rn(x[i], cs[e])), round_to<DT>(__fmul_rn(rot, sn[e]))));
-        }
-      }
-    }
+    float c0, c1, s0, s1;
+    unpack2<DT>(cos2, c0, c1);
+    unpack2<DT>(sin2, s0, s1);
+    x0 = round_to<DT>(__fadd_rn(round_to<DT>(__fmul_rn(x0, c0)), round_to<DT>(__fmul_rn(p0, s0))));
+    x1 = round_to<DT>(__fadd_rn(round_to<DT>(__fmul_rn(x1, c1)), round_to<DT>(__fmul_rn(p1, s1))));
   }
 }
 
@@ -233,6 +199,8 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   // APPEND: the new token's rows as the attention must see them (dequantised codes for fp8 caches)
   __shared__ uint4 s_new[APPEND ? 2 * R : 1];
   __shared__ float s_new_scale[APPEND && FP8 ? 2 : 1];
+  // QK: the prepared q rows and K row, as pairs of DT values
+  __shared__ uint32_t s_qk[QK ? (G + 1) * (D / 2) : 1];
 
   const int split = blockIdx.x;
   const int kvh = blockIdx.y;
@@ -302,26 +270,36 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
     new_raw[0] = *reinterpret_cast<const uint4*>(src + c * VEC);
     if constexpr (FP8) new_raw[1] = *reinterpret_cast<const uint4*>(src + c * VEC + 8);
   }
-  // QK: this lane's slices of the norm weights and of the sequence's cos/sin row, fetched with the first loads
-  // so that the prologue waits on no further memory round trip. Every load is issued on every path (a part
-  // that is not given reads q's row instead, never used) so that their waits stay exact.
-  QKSlices<VEC> qks;
+  // QK: the q/k preparation is spread over the workgroup, one pair of adjacent elements (d0, d0 + 1) per thread
+  // and round: the G q rows of this kv head, then the new K row, D/2 pairs each. This thread's pairs, their
+  // weights and the sequence's cos/sin pairs are fetched with the first loads (a part that is not given reads
+  // the q row instead, never used), so that the waits on them stay exact.
+  constexpr int kQKPairs = (G + 1) * (D / 2);
+  constexpr int kQKRounds = QK ? (kQKPairs + kBlockThreads - 1) / kBlockThreads : 1;
+  uint32_t qk_x[kQKRounds], qk_w[kQKRounds], qk_c[kQKRounds], qk_s[kQKRounds];
   const bool qk_norm_q = QK && p.q_norm_w != nullptr;
   const bool qk_norm_k = QK && p.k_norm_w != nullptr;
   const bool qk_rope = QK && p.rope_cos != nullptr;
   if constexpr (QK) {
-    const uint16_t* qrow = qb + kvh * G * p.q_stride_h;
-    const uint16_t* wq = qk_norm_q ? static_cast<const uint16_t*>(p.q_norm_w) : qrow;
-    const uint16_t* wk = qk_norm_k ? static_cast<const uint16_t*>(p.k_norm_w) : qrow;
-    const uint16_t* cr = qk_rope ? static_cast<const uint16_t*>(p.rope_cos) + b * p.rope_cos_stride_b : qrow;
-    const uint16_t* sr = qk_rope ? static_cast<const uint16_t*>(p.rope_sin) + b * p.rope_sin_stride_b : qrow;
+    const uint16_t* qrow = uniform_ptr(qb + kvh * G * p.q_stride_h);
+    const uint16_t* krow =
+        uniform_ptr(static_cast<const uint16_t*>(p.k_new) + b * p.kn_stride_b + kvh * p.kn_stride_h);
+    const uint16_t* wq = qk_norm_q ? uniform_ptr(static_cast<const uint16_t*>(p.q_norm_w)) : qrow;
+    const uint16_t* wk = qk_norm_k ? uniform_ptr(static_cast<const uint16_t*>(p.k_norm_w)) : qrow;
+    const uint16_t* cr =
+        qk_rope ? uniform_ptr(static_cast<const uint16_t*>(p.rope_cos) + b * p.rope_cos_stride_b) : qrow;
+    const uint16_t* sr =
+        qk_rope ? uniform_ptr(static_cast<const uint16_t*>(p.rope_sin) + b * p.rope_sin_stride_b) : qrow;
 #pragma unroll
-    for (int c = 0; c < VEC / 8; ++c) {
-      const int e = li * VEC + 8 * c;
-      qks.qw[c] = *reinterpret_cast<const uint4*>(wq + e);
-      qks.kw[c] = *reinterpret_cast<const uint4*>(wk + e);
-      qks.cs[c] = *reinterpret_cast<const uint4*>(cr + e);
-      qks.sn[c] = *reinterpret_cast<const uint4*>(sr + e);
+    for (int i = 0; i < kQKRounds; ++i) {
+      const int pp = min(tid + i * kBlockThreads, kQKPairs - 1);
+      const int r = pp / (D / 2);
+      const int d0 = 2 * (pp % (D / 2));
+      const uint16_t* x = r < G ? qrow + r * p.q_stride_h : krow;
+      qk_x[i] = *reinterpret_cast<const uint32_t*>(x + d0);
+      qk_w[i] = *reinterpret_cast<const uint32_t*>((r < G ? wq : wk) + d0);
+      qk_c[i] = *reinterpret_cast<const uint32_t*>(cr + d0);
+      qk_s[i] = *reinterpret_cast<const uint32_t*>(sr + d0);
     }
   }
 
@@ -420,24 +398,27 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
     first_entry = t_begin >> p.page_shift;
     const int n_ent = t_end > t_begin ? ((t_end - 1) >> p.page_shift) - first_entry + 1 : 0;
     const int32_t* bt = p.cache.block_table + static_cast<int64_t>(b) * p.cache.block_table_stride + first_entry;
-    // every load of the row first (one round trip), then the checks and the LDS writes
-    constexpr int kPer = (kMaxBlockEntries + kBlockThreads - 1) / kBlockThreads;
-    const int rounds = (n_ent + kBlockThreads - 1) / kBlockThreads;  // <= kPer
-    int32_t ent[kPer];
+    // up to four of a thread's entries in flight at once (one round trip for rows of up to 1024 entries), then
+    // the checks and the LDS writes
+    constexpr int kBatch = 4;
+    const int rounds = (n_ent + kBlockThreads - 1) / kBlockThreads;  // <= kMaxBlockEntries / kBlockThreads
+    for (int k0 = 0; k0 < rounds; k0 += kBatch) {
+      int32_t ent[kBatch];
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      if (k < rounds) ent[k] = bt[min(tid + k * kBlockThreads, n_ent - 1)];
-    }
+      for (int k = 0; k < kBatch; ++k) {
+        if (k0 + k < rounds) ent[k] = bt[min(tid + (k0 + k) * kBlockThreads, n_ent - 1)];
+      }
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int i = tid + k * kBlockThreads;
-      if (k < rounds && i < n_ent) {
-        int32_t blk = ent[k];
-        if (blk < 0 || blk >= p.cache.num_blocks) {
-          if (p.status) atomicOr(p.status, kStatusBlockOutOfRange);
-          blk = -1;
+      for (int k = 0; k < kBatch; ++k) {
+        const int i = tid + (k0 + k) * kBlockThreads;
+        if (k0 + k < rounds && i < n_ent) {
+          int32_t blk = ent[k];
+          if (blk < 0 || blk >= p.cache.num_blocks) {
+            if (p.status) atomicOr(p.status, kStatusBlockOutOfRange);
+            blk = -1;
+          }
+          s_bt[i] = blk;
         }
-        s_bt[i] = blk;
       }
     }
     __syncthreads();
@@ -557,38 +538,38 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   // The prologue work that needs the length: q's preparation (QK) and the staging of the new rows (APPEND). It
   // runs once the wave's first super-chunk is in flight, so that its latency covers the work.
   auto prologue_work = [&]() {
-    // QK: q as the model prepares it (its loads and the slices were issued before every load of the cache, so
-    // waiting for them leaves the first super-chunk in flight; the arithmetic overlaps its latency). Split 0
-    // also writes it to q_out.
+    // QK: q and the new K row as the model prepares them, one pair per thread and round (their loads were
+    // issued before every load of the cache, so waiting for them leaves the first super-chunk in flight), into
+    // LDS; split 0 also writes the prepared q to q_out. Then every lane takes its q slices from there.
     if constexpr (QK) {
-      {
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
-          float x[VEC];
-          if constexpr (!FP8) {
-#pragma unroll
-            for (int j = 0; j < VEC / 2; ++j) unpack2<Q_DT>(qp[h][j], x[2 * j], x[2 * j + 1]);
-          } else {
-#pragma unroll
-            for (int i = 0; i < VEC; ++i) x[i] = qf[h][i];
+      for (int i = 0; i < kQKRounds; ++i) {
+        const int pp = tid + i * kBlockThreads;
+        const int r = min(pp, kQKPairs - 1) / (D / 2);
+        const int d0 = 2 * (pp % (D / 2));
+        float x0, x1;
+        unpack2<Q_DT>(qk_x[i], x0, x1);
+        qk_pair<Q_DT, D>(x0, x1, d0, qk_w[i], r < G ? qk_norm_q : qk_norm_k, qk_c[i], qk_s[i], qk_rope,
+                         p.norm_eps);
+        const uint32_t packed = pack2<Q_DT>(x0, x1);
+        if (pp < kQKPairs) {
+          s_qk[pp] = packed;
+          if (r < G && p.q_out && split == 0) {
+            *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.q_out) + b * p.q_out_stride_b +
+                                         (kvh * G + r) * p.q_out_stride_h + d0) = packed;
           }
-          qk_prologue<Q_DT, D, R, VEC>(x, li, qks.qw, qk_norm_q, qks.cs, qks.sn, qk_rope, p.norm_eps);
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+#pragma unroll
+        for (int j = 0; j < VEC / 2; ++j) {
+          const uint32_t w = s_qk[h * (D / 2) + li * (VEC / 2) + j];
           if constexpr (!FP8) {
-#pragma unroll
-            for (int j = 0; j < VEC / 2; ++j) qp[h][j] = pack2<Q_DT>(x[2 * j], x[2 * j + 1]);
+            qp[h][j] = w;
           } else {
-#pragma unroll
-            for (int i = 0; i < VEC; ++i) qf[h][i] = x[i];
-          }
-          if (p.q_out && split == 0 && tid < R) {
-            uint16_t* dst = static_cast<uint16_t*>(p.q_out) + b * p.q_out_stride_b + (kvh * G + h) * p.q_out_stride_h +
-                            li * VEC;
-#pragma unroll
-            for (int c = 0; c < VEC / 8; ++c) {
-              *reinterpret_cast<uint4*>(dst + 8 * c) =
-                  make_uint4(pack2<Q_DT>(x[8 * c], x[8 * c + 1]), pack2<Q_DT>(x[8 * c + 2], x[8 * c + 3]),
-                             pack2<Q_DT>(x[8 * c + 4], x[8 * c + 5]), pack2<Q_DT>(x[8 * c + 6], x[8 * c + 7]));
-            }
+            unpack2<Q_DT>(w, qf[h][2 * j], qf[h][2 * j + 1]);
           }
         }
       }
@@ -602,22 +583,13 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
       if (t_new >= 0 && tid < 2 * R) {
         const int which = tid / R;  // 0 = K, 1 = V
         const int c = tid % R;
-        // QK: the new K row as the model prepares it (the whole K row group, lanes 0..R-1 with li == c, takes
-        // this branch)
+        // QK: the new K row as prepared above
         if (QK && which == 0) {
           constexpr int NW = FP8 ? 2 : 1;
-          float x[VEC];
 #pragma unroll
           for (int n = 0; n < NW; ++n) {
-            const uint32_t w[4] = {new_raw[n].x, new_raw[n].y, new_raw[n].z, new_raw[n].w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) unpack2<Q_DT>(w[j], x[8 * n + 2 * j], x[8 * n + 2 * j + 1]);
-          }
-          qk_prologue<Q_DT, D, R, VEC>(x, c, qks.kw, qk_norm_k, qks.cs, qks.sn, qk_rope, p.norm_eps);
-#pragma unroll
-          for (int n = 0; n < NW; ++n) {
-            new_raw[n] = make_uint4(pack2<Q_DT>(x[8 * n], x[8 * n + 1]), pack2<Q_DT>(x[8 * n + 2], x[8 * n + 3]),
-                                    pack2<Q_DT>(x[8 * n + 4], x[8 * n + 5]), pack2<Q_DT>(x[8 * n + 6], x[8 * n + 7]));
+            const uint32_t* kp = s_qk + G * (D / 2) + c * (VEC / 2) + 4 * n;
+            new_raw[n] = make_uint4(kp[0], kp[1], kp[2], kp[3]);
           }
         }
         int64_t blk = b;
