@@ -289,6 +289,9 @@ int run_decode(const DecodeCall& c, hipStream_t stream) {
   p.scale_log2 = c.sm_scale * 1.4426950408889634f;
   p.ws_counter = reinterpret_cast<int32_t*>(ws + kArrivalOff);
   p.ws_arrive = reinterpret_cast<int32_t*>(ws + kBatchArriveOff);
+  // Every workgroup of a batch row counts itself in on that row's counter; counters sharing a cache line
+  // serialise each other's atomics, so each row gets a 128-byte line of its own while the region allows.
+  p.arrive_stride = static_cast<int32_t>(std::min<int64_t>(32, kMaxPairs / c.batch));
   p.ws_ml = reinterpret_cast<float*>(ws + pl.ml_off);
   p.ws_acc = reinterpret_cast<float*>(ws + pl.acc_off);
   p.status = c.status;

@@ -66,7 +66,8 @@ struct DecodeParams {
   float* ws_ml;        // [B * Hq * max_splits][2]  (m, l)
   float* ws_acc;       // [B * Hq * max_splits][D]
   int32_t* ws_counter; // [B * Hkv] split arrivals, zero between launches
-  int32_t* ws_arrive;  // [B] APPEND: workgroups that have read positions[b], zero between launches
+  int32_t* ws_arrive;  // [B * arrive_stride] APPEND: readers of positions[b], zero between launches
+  int32_t arrive_stride;  // int32 slots between batch rows' counters (32: one 128-byte line each)
   int32_t* status;
   // APPEND only
   const void* k_new;
@@ -348,10 +349,11 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
     if constexpr (APPEND) {
       if (tid == 0 && p.seq_lens_out) {
         const int readers = gridDim.x * gridDim.y;
-        const int prev = __hip_atomic_fetch_add(p.ws_arrive + b, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        int32_t* const arrive = p.ws_arrive + static_cast<int64_t>(b) * p.arrive_stride;
+        const int prev = __hip_atomic_fetch_add(arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (prev == readers - 1) {
           p.seq_lens_out[b] = len_read + 1;
-          __hip_atomic_store(p.ws_arrive + b, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(arrive, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       }
     }
