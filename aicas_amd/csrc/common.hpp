@@ -58,6 +58,18 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
   }
 }
 
+// Two OCP e4m3 codes of w (bytes 0-1, or 2-3 when HI) -> the same two values in the 16-bit type DT, packed
+// lo in the low half. Exact: every e4m3 value (subnormals included) is a bf16 and an fp16 value. One
+// v_cvt_scalef32_pk_{bf16,f16}_fp8 with unit scale on gfx950.
+template <int DT, bool HI>
+__device__ __forceinline__ uint32_t e4m3x2_to_16(uint32_t w) {
+  if constexpr (DT == kBF16) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
+  } else {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, HI));
+  }
+}
+
 // float -> bf16 bits, round to nearest even, NaN kept NaN (torch's float->bfloat16 rule): one
 // v_cvt_pk_bf16_f32 on gfx950.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f)); }

@@ -213,26 +213,19 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
 
   // Query slices of the G heads served by this kv head (independent of the lengths: issued first).
   const uint16_t* qb = static_cast<const uint16_t*>(p.q) + b * p.q_stride_b;
-  uint32_t qp[G][FP8 ? 1 : VEC / 2];
-  float qf[G][FP8 ? VEC : 1];
+  // (VEC / 2 pairs of q's 16-bit type per lane; fp8 caches take their K codes to the same type, exactly, so
+  // that both dot products run on v_dot2)
+  uint32_t qp[G][VEC / 2];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     const uint16_t* qh = qb + (kvh * G + h) * p.q_stride_h + li * VEC;
-    if constexpr (!FP8) {
-      const uint4 w = *reinterpret_cast<const uint4*>(qh);
-      qp[h][0] = w.x;
-      qp[h][1] = w.y;
-      qp[h][2] = w.z;
-      qp[h][3] = w.w;
-    } else {
 #pragma unroll
-      for (int c = 0; c < VEC / 8; ++c) {
-        const uint4 w = *reinterpret_cast<const uint4*>(qh + 8 * c);
-        unpack2<Q_DT>(w.x, qf[h][8 * c + 0], qf[h][8 * c + 1]);
-        unpack2<Q_DT>(w.y, qf[h][8 * c + 2], qf[h][8 * c + 3]);
-        unpack2<Q_DT>(w.z, qf[h][8 * c + 4], qf[h][8 * c + 5]);
-        unpack2<Q_DT>(w.w, qf[h][8 * c + 6], qf[h][8 * c + 7]);
-      }
+    for (int c = 0; c < VEC / 8; ++c) {
+      const uint4 w = *reinterpret_cast<const uint4*>(qh + 8 * c);
+      qp[h][4 * c + 0] = w.x;
+      qp[h][4 * c + 1] = w.y;
+      qp[h][4 * c + 2] = w.z;
+      qp[h][4 * c + 3] = w.w;
     }
   }
 
@@ -469,22 +462,19 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
           s[u][h] = group_sum<R>(d) * p.scale_log2;
         }
       } else {
-        float kf[VEC];
+        // the 16 codes as 8 exact pairs of q's type, then v_dot2 as for 16-bit caches
         const uint32_t kw[4] = {c.k[u].x, c.k[u].y, c.k[u].z, c.k[u].w};
+        uint32_t k2[VEC / 2];
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-          const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(kw[w]), false);
-          const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(kw[w]), true);
-          kf[4 * w + 0] = lo.x;
-          kf[4 * w + 1] = lo.y;
-          kf[4 * w + 2] = hi.x;
-          kf[4 * w + 3] = hi.y;
+          k2[2 * w] = e4m3x2_to_16<Q_DT, false>(kw[w]);
+          k2[2 * w + 1] = e4m3x2_to_16<Q_DT, true>(kw[w]);
         }
 #pragma unroll
         for (int h = 0; h < G; ++h) {
           float d = 0.0f;
 #pragma unroll
-          for (int i = 0; i < VEC; ++i) d = fmaf(qf[h][i], kf[i], d);
+          for (int j = 0; j < VEC / 2; ++j) d = dot2<Q_DT>(qp[h][j], k2[j], d);
           s[u][h] = group_sum<R>(d) * (p.scale_log2 * c.ks[u]);
         }
       }
@@ -566,12 +556,7 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
       for (int h = 0; h < G; ++h) {
 #pragma unroll
         for (int j = 0; j < VEC / 2; ++j) {
-          const uint32_t w = s_qk[h * (D / 2) + li * (VEC / 2) + j];
-          if constexpr (!FP8) {
-            qp[h][j] = w;
-          } else {
-            unpack2<Q_DT>(w, qf[h][2 * j], qf[h][2 * j + 1]);
-          }
+          qp[h][j] = s_qk[h * (D / 2) + li * (VEC / 2) + j];
         }
       }
     }
