@@ -168,12 +168,13 @@ __device__ __forceinline__ T* uniform_ptr(T* ptr) {
   return (T*)g;
 }
 
-template <int KV_DT, int U>
+// U loads of K and of V rows per lane, the rows' validity and, for fp8 caches, the chunk's per-token scales
+// (NSW words per lane, see load_rows).
+template <int U, int NSW>
 struct Chunk {
   uint4 k[U];
   uint4 v[U];
-  float ks[U];
-  float vs[U];
+  float sc[NSW];
   bool ok[U];
 };
 
@@ -189,6 +190,9 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   constexpr int RPB = RPW * kWavesPerBlock;
   static_assert(R >= 1 && R <= 16, "a row must fit one DPP row");
   constexpr bool FP8 = (KV_DT == kFP8E4M3);
+  constexpr int NS = U * RPW;                                 // tokens per wave chunk
+  constexpr int NSW = FP8 ? (2 * NS + kWave - 1) / kWave : 1;  // fp8: scale words per lane per chunk
+  using ChunkT = Chunk<U, NSW>;
 
   __shared__ float s_m[kWavesPerBlock][G];
   __shared__ float s_l[kWavesPerBlock][G];
@@ -301,7 +305,9 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   // an invalid page), so that every load is issued on every path and the compiler can wait for one buffer
   // while the other stays in flight. Their words are never let through by consume. A chunk that is not
   // `valid` (no such chunk) loads row t_dummy of block 0 / of the sequence in every lane, all masked.
-  auto load_rows = [&](Chunk<KV_DT, U>& c, int t0, int hi, int skip, int first_entry, bool valid, int t_dummy) {
+  const float* const kscale = FP8 ? uniform_ptr(p.cache.k_scale) : nullptr;
+  const float* const vscale = FP8 ? uniform_ptr(p.cache.v_scale) : nullptr;
+  auto load_rows = [&](ChunkT& c, int t0, int hi, int skip, int first_entry, bool valid, int t_dummy) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int t = t0 + u * RPW + row;
@@ -318,16 +324,31 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
       const int64_t off = blk * p.cache.stride_blk + head_off + static_cast<int64_t>(tin) * p.cache.stride_t;
       c.k[u] = *reinterpret_cast<const uint4*>(kbase + off * EB + li * 16);
       c.v[u] = *reinterpret_cast<const uint4*>(vbase + off * EB + li * 16);
-      if constexpr (FP8) {
-        const int64_t soff = blk * p.cache.scale_stride_blk + shead_off + tin;
-        c.ks[u] = p.cache.k_scale[soff];
-        c.vs[u] = p.cache.v_scale[soff];
-      }
       c.ok[u] = ok;
+    }
+    // fp8: the chunk's scales in one load per lane (not one per row and lane): word j of lane l holds entry
+    // j * 64 + l of [the K scales of tokens t0 .. t0 + NS - 1, then their V scales] (entries past 2 NS repeat
+    // the last one, unused); consume fetches each row's pair from the lanes holding them with a shuffle.
+    if constexpr (FP8) {
+#pragma unroll
+      for (int j = 0; j < NSW; ++j) {
+        const int i = min(j * kWave + lane, 2 * NS - 1);
+        const bool is_v = i >= NS;
+        const int t = t0 + (is_v ? i - NS : i);
+        const int tc = valid ? min(t, hi - 1) : t_dummy;
+        int64_t blk = b;
+        int tin = tc;
+        if constexpr (PAGED) {
+          const int32_t e = s_bt[(tc >> p.page_shift) - first_entry];
+          blk = valid && e >= 0 ? e : 0;
+          tin = tc & page_mask;
+        }
+        c.sc[j] = (is_v ? vscale : kscale)[blk * p.cache.scale_stride_blk + shead_off + tin];
+      }
     }
   };
 
-  Chunk<KV_DT, U> ca, cb;
+  ChunkT ca, cb;
 
   // Sequence length (cached tokens before this step's append for APPEND).
   if (tid == 0) s_len = p.seq_lens ? p.seq_lens[b] : p.uniform_len;
@@ -430,7 +451,7 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   // The wave's first super-chunk goes out now, before the prologue work below; a wave without one loads a
   // masked dummy (every row reads token t_begin, whose block entry is staged whenever a chunk could exist),
   // so that every load is issued on every path and the waits on the buffers stay exact.
-  auto load_chunk = [&](Chunk<KV_DT, U>& c, int t0, bool valid) {
+  auto load_chunk = [&](ChunkT& c, int t0, bool valid) {
     load_rows(c, valid ? t0 : t_begin, t_end, t_new, first_entry, valid, t_begin);
   };
   const int sc0 = super_start(0);
@@ -446,7 +467,16 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
     for (int i = 0; i < VEC; ++i) acc[h][i] = 0.0f;
   }
 
-  auto consume = [&](const Chunk<KV_DT, U>& c) {
+  auto consume = [&](const ChunkT& c) {
+    // fp8: each row's K and V scales, from the lanes that loaded them (see load_rows)
+    float ks[U], vs[U];
+    if constexpr (FP8) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        ks[u] = __shfl(c.sc[(u * RPW) / kWave], (u * RPW + row) % kWave);
+        vs[u] = __shfl(c.sc[(NS + u * RPW) / kWave], (NS + u * RPW + row) % kWave);
+      }
+    }
     // Scores (log2 domain) for U tokens x G heads.
     float s[U][G];
 #pragma unroll
@@ -475,7 +505,7 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
           float d = 0.0f;
 #pragma unroll
           for (int j = 0; j < VEC / 2; ++j) d = dot2<Q_DT>(qp[h][j], k2[j], d);
-          s[u][h] = group_sum<R>(d) * (p.scale_log2 * c.ks[u]);
+          s[u][h] = group_sum<R>(d) * (p.scale_log2 * ks[u]);
         }
       }
 #pragma unroll
@@ -519,7 +549,7 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
       for (int h = 0; h < G; ++h) {
         const float pu = fast_exp2(s[u][h] - mnew[h]);
         l[h] += pu;
-        const float pv = FP8 ? (c.ok[u] ? pu * c.vs[u] : 0.0f) : pu;
+        const float pv = FP8 ? (c.ok[u] ? pu * vs[u] : 0.0f) : pu;
 #pragma unroll
         for (int i = 0; i < VEC; ++i) acc[h][i] = fmaf(pv, vf[i], acc[h][i]);
       }
@@ -634,7 +664,7 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   // in just before the chunk is consumed, when its loads have landed anyway (only the chunk holding it takes
   // this branch). The token is thus attended to at its place in the stream, exactly as a separate append
   // followed by attention would.
-  auto take_new_row = [&](Chunk<KV_DT, U>& c, int t0) {
+  auto take_new_row = [&](ChunkT& c, int t0) {
     if constexpr (APPEND) {
       if (t_new >= t0 && t_new < t0 + CW) {
 #pragma unroll
@@ -642,11 +672,15 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
           if (t0 + u * RPW + row == t_new) {
             c.k[u] = s_new[li];
             c.v[u] = s_new[R + li];
-            if constexpr (FP8) {
-              c.ks[u] = s_new_scale[0];
-              c.vs[u] = s_new_scale[1];
-            }
             c.ok[u] = true;
+          }
+        }
+        if constexpr (FP8) {
+          const int ik = t_new - t0;  // its K scale is entry ik of the chunk's scales, its V scale NS + ik
+#pragma unroll
+          for (int j = 0; j < NSW; ++j) {
+            if (j * kWave + lane == ik) c.sc[j] = s_new_scale[0];
+            if (j * kWave + lane == NS + ik) c.sc[j] = s_new_scale[1];
           }
         }
       }
