@@ -198,7 +198,6 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   __shared__ float s_l[kWavesPerBlock][G];
   __shared__ float s_acc[kWavesPerBlock][G][D];
   __shared__ int32_t s_bt[PAGED ? kMaxBlockEntries : 1];
-  __shared__ int32_t s_len;
   __shared__ int32_t s_last;
   // APPEND: the new token's rows as the attention must see them (dequantised codes for fp8 caches)
   __shared__ uint4 s_new[APPEND ? 2 * R : 1];
@@ -350,14 +349,22 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
 
   ChunkT ca, cb;
 
-  // Sequence length (cached tokens before this step's append for APPEND).
-  if (tid == 0) s_len = p.seq_lens ? p.seq_lens[b] : p.uniform_len;
-  __syncthreads();
-  int L = s_len;
+  // Sequence length (cached tokens before this step's append for APPEND), read by every wave: a uniform load,
+  // so its wait does not cover the vector loads issued after it.
+  int L = p.seq_lens ? p.seq_lens[b] : p.uniform_len;
   const int len_read = L;
-  // APPEND with seq_lens_out: every workgroup counts itself in on its way out (thread 0's read of positions[b]
-  // completed long before: its value went to LDS ahead of the barrier above); the last of the batch row's
-  // workgroups stores the bumped length, so no workgroup can read it. Counting in at exit keeps the
+  // Contiguous caches: a wave's first super-chunk in the striped schedule (super-chunk wave_slot) does not depend
+  // on the length, so both buffers go out now, rows clamped to the capacity (always inside the cache); the rows'
+  // validity is settled once the length is known. Paged caches need the block table first.
+  constexpr bool kSpec = !PAGED;
+  const int spec_t0 = wave_slot * SCW;
+  if constexpr (kSpec) {
+    load_rows(ca, spec_t0, p.cache.max_tokens, -1, 0, true, 0);
+    load_rows(cb, spec_t0 + CW, p.cache.max_tokens, -1, 0, true, 0);
+  }
+  // APPEND with seq_lens_out: every workgroup counts itself in on its way out (each of its waves' reads of
+  // positions[b] completed long before: every wave used the value to plan its work); the last of the batch
+  // row's workgroups stores the bumped length, so no workgroup can read it. Counting in at exit keeps the
   // contended atomic off the start of the stream.
   auto count_in = [&]() {
     if constexpr (APPEND) {
@@ -455,8 +462,19 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
     load_rows(c, valid ? t0 : t_begin, t_end, t_new, first_entry, valid, t_begin);
   };
   const int sc0 = super_start(0);
-  load_chunk(ca, sc0, sc0 >= 0);
-  load_chunk(cb, sc0 + CW, sc0 >= 0);
+  if constexpr (kSpec) {
+    // striped: sc0 is spec_t0 when the wave has a first super-chunk; its rows count if they lie below the length
+    // and are not the new token's (whose row is swapped in before the chunk is consumed)
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int t = spec_t0 + u * RPW + row;
+      ca.ok[u] = sc0 >= 0 && t < t_end && t != t_new;
+      cb.ok[u] = sc0 >= 0 && t + CW < t_end && t + CW != t_new;
+    }
+  } else {
+    load_chunk(ca, sc0, sc0 >= 0);
+    load_chunk(cb, sc0 + CW, sc0 >= 0);
+  }
 
   float m[G], l[G], acc[G][VEC];
 #pragma unroll
