@@ -235,6 +235,7 @@ struct DecodeCall {
   const int32_t* lens;
   int32_t uniform_len;
   int32_t bound;
+  int32_t min_attended;  // caller's lower bound on every attended length (0: none)
   int32_t batch, num_q_heads, num_kv_heads, head_dim;
   float sm_scale;
   int32_t tokens_per_split;
@@ -285,6 +286,12 @@ int run_decode(const DecodeCall& c, hipStream_t stream) {
   p.num_kv_heads = c.num_kv_heads;
   p.tokens_per_split = pl.tokens_per_split;
   p.max_splits = pl.num_splits;
+  // Splits that every sequence keeps busy by the caller's lower bound: they may fetch their first rows before
+  // reading the length. A wrong bound only costs bandwidth: the rows' validity always comes from the length.
+  p.spec_splits = c.min_attended > 0
+                      ? static_cast<int32_t>(std::min<int64_t>(pl.num_splits,
+                                                                ceil_div(int64_t{c.min_attended}, pl.tokens_per_split)))
+                      : 0;
   p.page_shift = c.cache->block_table ? ilog2(c.cache->page_size) : 0;
   p.scale_log2 = c.sm_scale * 1.4426950408889634f;
   p.ws_counter = reinterpret_cast<int32_t*>(ws + kArrivalOff);
@@ -357,7 +364,7 @@ int decode_append(const aicas_kv_cache_t* cache, const aicas_qk_prologue_t* pro,
   c.out_stride_h = out_stride_h;
   c.lens = positions;
   c.uniform_len = 0;
-  (void)min_len;  // a hint the kernels do not need: they read every length on the device
+  c.min_attended = min_len > 0 ? min_len + 1 : 0;  // positions[b] >= min_len: the new token makes min_len + 1
   c.bound = max_seq_len;
   c.batch = batch;
   c.num_q_heads = num_q_heads;
@@ -461,7 +468,7 @@ int aicas_decode_attention(const aicas_kv_cache_t* cache, int32_t q_dtype, const
   c.out_stride_h = out_stride_h;
   c.lens = seq_lens;
   c.uniform_len = uniform_len;
-  (void)min_len;
+  c.min_attended = seq_lens ? (min_len > 0 ? min_len : 0) : uniform_len;
   c.bound = seq_lens ? max_seq_len : uniform_len;
   c.batch = batch;
   c.num_q_heads = num_q_heads;

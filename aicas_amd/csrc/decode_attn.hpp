@@ -61,6 +61,7 @@ struct DecodeParams {
   int32_t num_kv_heads;
   int32_t tokens_per_split;
   int32_t max_splits;  // == gridDim.x
+  int32_t spec_splits; // splits every sequence keeps busy by the caller's lower bound on the lengths
   int32_t page_shift;  // log2(page_size) for paged caches
   float scale_log2;    // sm_scale * log2(e)
   float* ws_ml;        // [B * Hq * max_splits][2]  (m, l)
@@ -178,9 +179,10 @@ struct Chunk {
   bool ok[U];
 };
 
-template <int Q_DT, int KV_DT, int D, int G, bool PAGED, bool APPEND, bool QK>
+template <int Q_DT, int KV_DT, int D, int G, bool PAGED, bool APPEND, bool QK, bool SPEC>
 __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams p) {
   static_assert(APPEND || !QK, "the q/k prologue belongs to the fused append");
+  static_assert(!(SPEC && PAGED), "only contiguous caches fetch rows before the length is known");
   using Tr = KVTraits<KV_DT>;
   constexpr int EB = Tr::kElemBytes;
   constexpr int VEC = Tr::kVec;
@@ -353,12 +355,13 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   // so its wait does not cover the vector loads issued after it.
   int L = p.seq_lens ? p.seq_lens[b] : p.uniform_len;
   const int len_read = L;
-  // Contiguous caches: a wave's first super-chunk in the striped schedule (super-chunk wave_slot) does not depend
-  // on the length, so both buffers go out now, rows clamped to the capacity (always inside the cache); the rows'
-  // validity is settled once the length is known. Paged caches need the block table first.
-  constexpr bool kSpec = !PAGED;
+  // SPEC (contiguous caches, launched when the caller's lower bound on the lengths keeps every split busy): a
+  // wave's first super-chunk in the striped schedule (super-chunk wave_slot) does not depend on the length, so
+  // both buffers go out now, rows clamped to the capacity (always inside the cache), and the rows' validity is
+  // settled once the length is known. Otherwise (and for paged caches, which need the block table first) the
+  // first rows are fetched once the length is known.
   const int spec_t0 = wave_slot * SCW;
-  if constexpr (kSpec) {
+  if constexpr (SPEC) {
     load_rows(ca, spec_t0, p.cache.max_tokens, -1, 0, true, 0);
     load_rows(cb, spec_t0 + CW, p.cache.max_tokens, -1, 0, true, 0);
   }
@@ -462,7 +465,7 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
     load_rows(c, valid ? t0 : t_begin, t_end, t_new, first_entry, valid, t_begin);
   };
   const int sc0 = super_start(0);
-  if constexpr (kSpec) {
+  if constexpr (SPEC) {
     // striped: sc0 is spec_t0 when the wave has a first super-chunk; its rows count if they lie below the length
     // and are not the new token's (whose row is swapped in before the chunk is consumed)
 #pragma unroll

@@ -7,12 +7,26 @@
 
 namespace aicas {
 
+template <int Q, int KV, int D, int G, bool PAGED, bool SPEC>
+void launch_decode_dgps(const DecodeParams& p, bool append, bool qk, dim3 grid, hipStream_t s) {
+  const dim3 block(kBlockThreads);
+  if (qk) hipLaunchKernelGGL((decode_attn_kernel<Q, KV, D, G, PAGED, true, true, SPEC>), grid, block, 0, s, p);
+  else if (append)
+    hipLaunchKernelGGL((decode_attn_kernel<Q, KV, D, G, PAGED, true, false, SPEC>), grid, block, 0, s, p);
+  else hipLaunchKernelGGL((decode_attn_kernel<Q, KV, D, G, PAGED, false, false, SPEC>), grid, block, 0, s, p);
+}
+
+// Contiguous caches whose every split is kept busy by the caller's lower bound on the lengths take the variant
+// that fetches its first rows before reading the length.
 template <int Q, int KV, int D, int G, bool PAGED>
 void launch_decode_dgp(const DecodeParams& p, bool append, bool qk, dim3 grid, hipStream_t s) {
-  const dim3 block(kBlockThreads);
-  if (qk) hipLaunchKernelGGL((decode_attn_kernel<Q, KV, D, G, PAGED, true, true>), grid, block, 0, s, p);
-  else if (append) hipLaunchKernelGGL((decode_attn_kernel<Q, KV, D, G, PAGED, true, false>), grid, block, 0, s, p);
-  else hipLaunchKernelGGL((decode_attn_kernel<Q, KV, D, G, PAGED, false, false>), grid, block, 0, s, p);
+  if constexpr (!PAGED) {
+    if (p.spec_splits >= p.max_splits) {
+      launch_decode_dgps<Q, KV, D, G, false, true>(p, append, qk, grid, s);
+      return;
+    }
+  }
+  launch_decode_dgps<Q, KV, D, G, PAGED, false>(p, append, qk, grid, s);
 }
 
 template <int Q, int KV, int D, int G>

@@ -327,9 +327,10 @@ def decode_attention(
     """q ``[B, Hq, 1, D]`` (or ``[B, Hq, D]``) -> out of the same shape, attending to each sequence's cache.
 
     ``seq_lens`` (int32 ``[B]``, on device) gives per-sequence lengths; ``max_seq_len`` must bound them.
-    ``min_seq_len`` (optional) is a lower bound the caller may pass; the kernel reads every length on the device
-    and does not use it. Without ``seq_lens`` every sequence has ``max_seq_len`` tokens (default: the cache
-    capacity).
+    ``min_seq_len`` (optional) is a lower bound on the lengths the caller may pass: when it keeps every split of a
+    contiguous cache busy, the launch fetches its first rows before reading the lengths. Results never depend on
+    it (a wrong bound costs bandwidth only). Without ``seq_lens`` every sequence has ``max_seq_len`` tokens
+    (default: the cache capacity).
     """
     squeeze = q.dim() == 3
     q4 = q.unsqueeze(2) if squeeze else q
@@ -433,9 +434,10 @@ def decode_attention_append(
 ) -> torch.Tensor:
     """One decode step in one launch: append ``k_new``/``v_new`` (``[B, Hkv, 1, D]`` or ``[B, Hkv, D]``) at
     ``positions[b]`` and attend over ``positions[b] + 1`` tokens. ``seq_lens_out[b] = positions[b] + 1`` (it
-    may be ``positions`` itself). ``max_seq_len`` bounds ``positions[b] + 1``; ``min_seq_len`` (optional, unused
-    by the kernel) is a lower bound on every ``positions[b]``. With ``qk``, q and ``k_new`` are the projections' outputs and are
-    normalised and rotated as the model does before use (``aicas_decode_attention_append_qk``)."""
+    may be ``positions`` itself). ``max_seq_len`` bounds ``positions[b] + 1``; ``min_seq_len`` (optional) is a
+    lower bound on every ``positions[b]``, used as by :func:`decode_attention`. With ``qk``, q and ``k_new`` are
+    the projections' outputs and are normalised and rotated as the model does before use
+    (``aicas_decode_attention_append_qk``)."""
     squeeze = q.dim() == 3
     q4 = q.unsqueeze(2) if squeeze else q
     if q4.dim() != 4 or q4.shape[2] != 1 or q4.stride(3) != 1:

@@ -122,8 +122,8 @@ int aicas_decode_plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int3
  * cache must have kv_dtype == q_dtype. max_seq_len must bound every L_b: longer sequences are clamped and
  * AICAS_STATUS_LEN_CLAMPED is set. An empty sequence (L_b == 0) yields zeros. head_dim in {16, 32, 64, 128},
  * G in {1, 2, 4, 8}. tokens_per_split as from aicas_decode_plan (0 = automatic). min_len is a lower bound on every
- * L_b that the caller may pass (0 if unknown). The kernels read every length on the device before their first
- * cache read and do not use it; results never depend on it.
+ * L_b that the caller may pass (0 if unknown): when it keeps every split of a contiguous cache busy, the launch
+ * fetches its first rows before reading the lengths. Results never depend on it; a wrong bound costs bandwidth.
  * Replaces: triton_qwen3vl/gqa_decode_attention.py:46-141, :268-327; dujunbaoV1/native_cuda_ops/
  * decode_q1_gqa.cpp:73-95; new KV cache/evaluation_wrapper.py:248-265.
  */
@@ -142,7 +142,7 @@ int aicas_decode_attention(const aicas_kv_cache_t* cache, int32_t q_dtype, const
  * aicas_kv_append followed by aicas_decode_attention would give. If seq_lens_out is not NULL,
  * seq_lens_out[b] = positions[b] + 1 is stored once every workgroup has read positions[b]; it may alias
  * positions. max_seq_len must bound positions[b] + 1; min_len (0 if unknown) is a lower bound on every
- * positions[b], unused as for aicas_decode_attention. A token with no slot left in the cache is dropped and
+ * positions[b], used as by aicas_decode_attention. A token with no slot left in the cache is dropped and
  * AICAS_STATUS_APPEND_OVERFLOW is set. The workspace must come from aicas_decode_plan with the same shapes.
  * Replaces the pair Qwen3VLTextAttention.forward issues per layer and step
  * (transformers/models/qwen3_vl/modeling_qwen3_vl.py:487-503): past_key_values.update (cache_utils.py:127-146)

@@ -258,6 +258,43 @@ def test_fp8_code_decode_matches_table(dev):
     assert torch.equal(out, expect)
 
 
+@pytest.mark.parametrize("tps", [64, 320])
+@pytest.mark.parametrize("lens, bound", [([2250, 2260, 2270, 2299], 2250),  # the true lower bound
+                                         ([5, 100, 2270, 2299], 2299)])      # a wrong one: idle splits fetch
+def test_early_fetch_variant_is_bitwise_the_ordered_launch(dev, tps, lens, bound):
+    """A lower bound that keeps every split of a contiguous cache busy selects the kernel variant that issues its
+    first rows before reading the lengths. Its output (and, fused, the cache and lengths) equals the ordered
+    launch's bit for bit, whether the bound is right or not: the rows' validity always comes from the lengths."""
+    gen = torch.Generator().manual_seed(78)
+    B, Hkv, G, D, cap = 4, 8, 2, 128, 2300
+    hi = max(lens)
+    plan = ops.decode_plan(torch.bfloat16, B, Hkv * G, Hkv, D, hi, 0, tps)
+    assert -(-bound // plan.tokens_per_split) >= plan.num_splits  # every split counts as busy: early-fetch variant
+    q = _rand((B, Hkv * G, 1, D), gen).to(dev)
+    view = ops.KVCacheView(_rand((B, Hkv, cap, D), gen).to(dev), _rand((B, Hkv, cap, D), gen).to(dev))
+    sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    base = ops.decode_attention(q, view, sm_scale=D ** -0.5, seq_lens=sl, max_seq_len=hi, tokens_per_split=tps)
+    early = ops.decode_attention(q, view, sm_scale=D ** -0.5, seq_lens=sl, max_seq_len=hi, min_seq_len=bound,
+                                 tokens_per_split=tps)
+    assert torch.equal(base.cpu(), early.cpu())
+    kd, vd = view.k.cpu().float(), view.v.cpu().float()
+    expect = ref.ragged_decode(q.cpu().float(), [kd[b, :, :lens[b]] for b in range(B)],
+                               [vd[b, :, :lens[b]] for b in range(B)], D ** -0.5, G).float()
+    torch.testing.assert_close(early.float().cpu(), expect, atol=2e-2, rtol=1e-2)
+    kn = _rand((B, Hkv, 1, D), gen).to(dev)
+    vn = _rand((B, Hkv, 1, D), gen).to(dev)
+    view_b = ops.KVCacheView(view.k.clone(), view.v.clone())
+    pos_a, pos_b = sl.clone(), sl.clone()
+    fa = ops.decode_attention_append(q, view, kn, vn, pos_a, sm_scale=D ** -0.5, max_seq_len=hi + 1,
+                                     seq_lens_out=pos_a, tokens_per_split=tps)
+    fb = ops.decode_attention_append(q, view_b, kn, vn, pos_b, sm_scale=D ** -0.5, max_seq_len=hi + 1,
+                                     min_seq_len=bound, seq_lens_out=pos_b, tokens_per_split=tps)
+    assert torch.equal(fa.cpu(), fb.cpu())
+    assert torch.equal(view.k.cpu().view(torch.int16), view_b.k.cpu().view(torch.int16))
+    assert torch.equal(view.v.cpu().view(torch.int16), view_b.v.cpu().view(torch.int16))
+    assert pos_a.cpu().tolist() == pos_b.cpu().tolist() == [L + 1 for L in lens]
+
+
 @pytest.mark.parametrize("tps", [0, 64, 320])
 def test_min_seq_len_hint_gives_identical_results(dev, tps):
     """A caller-guaranteed lower bound on the lengths only lets the kernel fetch early; results are unchanged."""
