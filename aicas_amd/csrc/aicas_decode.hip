@@ -165,9 +165,15 @@ int launch_decode(const aicas::DecodeParams& p, int q_dtype, int kv_dtype, int d
   return check_launch(APPEND ? "aicas_decode_attention_append" : "aicas_decode_attention");
 }
 
-// Workgroups per compute unit the split planner aims for, in quarters: 7/4 measured best on MI355X for the
-// 28-layer B=8 L=2048 decode (4 to 12 splits per (batch, kv head) pair within 7% of each other).
-constexpr int kWorkgroupsPerCUx4 = 7;
+// Workgroups per compute unit the split planner aims for, in quarters. Measured on MI355X (256 CUs), µs per
+// launch: B=8 L=2048 (64 (batch, kv head) pairs) 19.4 / 17.1 / 17.4 / 20.7 / 18.4 / 17.4 / 18.2 for 2 / 3 / 4 /
+// 5 / 6 / 7 / 8 splits per pair; B=1 L=32768 (8 pairs) 35.0 / 33.8 / 33.7 / 33.6 / 33.3 / 41.4 / 34.4 / 39.8 for
+// 17 / 20 / 24 / 28 / 31 / 33 / 56 / 65 splits; ragged B=32 paged fp8 (256 pairs) 86.8 / 80.9 / 91.3 for 1 / 2 / 4.
+// With few pairs: about 3/4 of a workgroup per CU and never more than one (a few CUs holding two workgroups
+// make the tail: 264 and 320 workgroups are the slow cases above). With many pairs (batches of ragged
+// lengths): 7/4, so that the longest sequences are split.
+constexpr int kFewPairsWGsPerCUx4 = 3;
+constexpr int kManyPairsWGsPerCUx4 = 7;
 
 // Workspace layout. The counters sit at fixed offsets, the same for every launch shape, ahead of the
 // partials: they are zero between launches whatever shapes ran before on the same workspace, since no launch
@@ -199,13 +205,18 @@ int plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int32_t num_kv_he
   if (hint > 0) {
     tps = ceil_div(hint, rpb) * rpb;
   } else {
-    // Split count: about kWorkgroupsPerCUx4 / 4 workgroups per compute unit in total.
+    // Split count: the workgroups per compute unit above, in total. A split covers at least one super-chunk
+    // (two chunks) per wave: below that its merge costs more than its streaming saves (B=1 L=1024: 17 splits
+    // 9.19 us, 9 splits 8.02 us).
     const int64_t pairs = int64_t{batch} * num_kv_heads;
-    const int64_t target = int64_t{kWorkgroupsPerCUx4} * device_cus() / 4;
-    const int64_t splits_wanted = std::max<int64_t>(1, (target + pairs / 2) / pairs);
+    const int64_t cus = device_cus();
+    const bool few = pairs * 4 <= int64_t{kFewPairsWGsPerCUx4} * cus;
+    const int64_t target = int64_t{few ? kFewPairsWGsPerCUx4 : kManyPairsWGsPerCUx4} * cus / 4;
+    int64_t splits_wanted = std::max<int64_t>(1, (target + pairs / 2) / pairs);
+    if (few) splits_wanted = std::max<int64_t>(1, std::min(splits_wanted, cus / pairs));
     tps = ceil_div(int64_t{max_seq_len > 0 ? max_seq_len : 1}, splits_wanted);
     tps = ceil_div(tps, rpb) * rpb;
-    if (tps < tpi) tps = tpi;
+    if (tps < 2 * tpi) tps = 2 * tpi;
   }
   // A split streaming a static range may touch at most kMaxBlockEntries block-table entries.
   if (page_size > 0) {

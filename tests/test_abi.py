@@ -89,6 +89,24 @@ def test_plan_covers_every_token(B, Hkv, L):
         assert wb >= parts * (128 + 2) * 4 + B * Hkv * 4 + B * 4
 
 
+@pytest.mark.skipif(__import__("torch").cuda.is_available(), reason="pins the plan for 256 compute units")
+def test_plan_split_counts():
+    """The planner's measured choices for 256 compute units: with few (batch, kv head) pairs about 3/4 of a
+    workgroup per CU and never more than one, with many pairs 7/4, and at least one super-chunk per wave."""
+    bf, f8 = _lib.DTYPE_BF16, _lib.DTYPE_FP8_E4M3
+    assert _plan(bf, 8, 16, 8, 128, 2176)[2] == 3      # B=8 L=2048 + 128 steps: 192 workgroups
+    assert _plan(bf, 1, 16, 8, 128, 32832)[2] == 24    # B=1 L=32768 + 64 steps
+    assert _plan(bf, 1, 16, 8, 128, 1025)[1:3] == (128, 9)  # B=1 L=1024: 128 tokens = 4 waves x 32
+    assert _plan(f8, 32, 16, 8, 128, 8193, 16)[2] == 2  # 256 pairs: 7/4 per CU
+    assert _plan(bf, 64, 16, 8, 128, 4097)[2] == 1     # 512 pairs
+    for B in range(1, 25):
+        for L in (300, 2049, 9000):
+            rc, tps, ns, _ = _plan(bf, B, 16, 8, 128, L)
+            assert rc == _lib.OK and tps >= 128
+            if B * 8 * 4 <= 3 * 256:
+                assert B * 8 * ns <= 256, (B, L, ns)
+
+
 def test_plan_honours_hint_and_rejects_bad_shapes():
     rc, tps, ns, _ = _plan(_lib.DTYPE_BF16, 8, 16, 8, 128, 2113, hint=300)
     assert rc == _lib.OK and tps == 304 and ns == 7
