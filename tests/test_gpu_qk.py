@@ -195,3 +195,45 @@ def test_hf_fused_decode_matches_dynamic_cache_sdpa(dev, kv_dtype, page_size):
     tol = 3e-2 if kv_dtype is None else 8e-2
     for a, b in zip(outs, ref_outs):
         assert float((a.float() - b.float()).norm() / b.float().norm()) < tol
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp16", "bf16_fp8"])
+def test_fused_qk_early_fetch_is_bitwise_the_ordered_launch(dev, kind):
+    """With a lower bound on the positions that keeps every split busy, the q/k step takes the early-fetch kernel
+    variant (contiguous caches); output, prepared q, cache rows and lengths equal the ordered launch's bit for bit."""
+    qdt = torch.float16 if kind.startswith("fp16") else torch.bfloat16
+    fp8 = "fp8" in kind
+    B, Hkv, G, D = 3, 8, 2, 128
+    Hq = Hkv * G
+    lens = [600, 610, 620]
+    cap = max(lens) + 1
+    plan = ops.decode_plan(ops.FP8_DTYPE if fp8 else qdt, B, Hq, Hkv, D, cap)
+    assert -(-(min(lens) + 1) // plan.tokens_per_split) >= plan.num_splits  # early-fetch variant
+    g = torch.Generator().manual_seed(5 + len(kind))
+    q = (3 * torch.randn((B, Hq, 1, D), generator=g)).to(qdt).to(dev)
+    k = (3 * torch.randn((B, Hkv, 1, D), generator=g)).to(qdt).to(dev)
+    v = torch.randn((B, Hkv, 1, D), generator=g).to(qdt).to(dev)
+    qw = (1 + 0.2 * torch.randn(D, generator=g)).to(qdt).to(dev)
+    kw = (1 + 0.2 * torch.randn(D, generator=g)).to(qdt).to(dev)
+    cos, sin = (t.to(dev) for t in _rope_rows(B, D, lens, qdt))
+    store = ops.FP8_DTYPE if fp8 else qdt
+    prefix_k = torch.randn((B, Hkv, max(lens), D), generator=g).to(qdt).to(dev)
+    prefix_v = torch.randn((B, Hkv, max(lens), D), generator=g).to(qdt).to(dev)
+    results = []
+    for bound in (0, min(lens)):
+        kc = torch.zeros((B, Hkv, cap, D), dtype=store, device=dev)
+        vc = torch.zeros_like(kc)
+        ks = torch.zeros((B, Hkv, cap), dtype=torch.float32, device=dev) if fp8 else None
+        vs = torch.zeros_like(ks) if fp8 else None
+        view = ops.KVCacheView(kc, vc, ks, vs)
+        ops.kv_append(view, prefix_k, prefix_v, torch.zeros(B, dtype=torch.int32, device=dev))
+        pos = torch.tensor(lens, dtype=torch.int32, device=dev)
+        q_out = torch.zeros((B, Hq, 1, D), dtype=qdt, device=dev)
+        qk = ops.QKPrologue(q_norm_weight=qw, k_norm_weight=kw, eps=1e-6, cos=cos, sin=sin, q_out=q_out)
+        out = ops.decode_attention_append(q, view, k, v, pos, sm_scale=D ** -0.5, max_seq_len=cap,
+                                          min_seq_len=bound, seq_lens_out=pos, qk=qk)
+        torch.cuda.synchronize()
+        results.append([t.cpu() for t in (out, q_out, kc.view(torch.uint8), vc.view(torch.uint8), pos)]
+                       + ([ks.cpu(), vs.cpu()] if fp8 else []))
+    for a, b in zip(*results):
+        assert torch.equal(a, b)
