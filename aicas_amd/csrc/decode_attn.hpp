@@ -30,10 +30,12 @@
 // split write the output directly.
 //
 // Prologue: q, the new rows (APPEND) and the q/k preparation's inputs, weights and rotary rows (QK) are fetched
-// before the lengths are read, so that their latencies overlap; once the length is known the wave's first
-// super-chunk (both buffers) is in flight before any other prologue work (the q/k preparation, the new rows'
-// staging) starts. Every load before the token loop is issued on every path, and no loaded register is written
-// before it is consumed, so that the compiler's waits are exact: waiting for one buffer never drains the other.
+// before the lengths are read, so that their latencies overlap; every wave reads its sequence's length with a
+// scalar load. The wave's first super-chunk (both buffers) is in flight before any other prologue work (the q/k
+// preparation, the new rows' staging) starts: with SPEC (contiguous caches whose every split has work by the
+// caller's bound) it is issued before the length arrives, since in the striped schedule it does not depend on
+// it. Every load before the token loop is issued on every path, and no loaded register is written before it is
+// consumed, so that the compiler's waits are exact: waiting for one buffer never drains the other.
 //
 // Fused append (APPEND): positions[b] is the length before this step; the kernel attends over
 // L_b = positions[b] + 1 tokens, of which token L_b - 1 comes from the new rows (k_new / v_new) instead of the
