@@ -548,33 +548,54 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
       for (int i = 0; i < VEC; ++i) acc[h][i] *= alpha[h];
       m[h] = mnew[h];
     }
+    // P.V on v_dot2, two tokens at a time: each element's two values (one per token) form one operand and the
+    // two tokens' probabilities, rounded to q's 16-bit type (as the reference's Triton kernel rounds P before
+    // its product with V), the other; products are exact and accumulate in fp32. fp8 rows are first taken to
+    // q's type exactly, their per-row scales folded into P.
+    static_assert(U % 2 == 0, "tokens are paired");
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float vf[VEC];
-      // a masked row's weight is 0, but its registers hold stale words that must not reach the FMA as NaN/Inf
-      const uint32_t vw[4] = {c.ok[u] ? c.v[u].x : 0u, c.ok[u] ? c.v[u].y : 0u, c.ok[u] ? c.v[u].z : 0u,
+    for (int u = 0; u < U; u += 2) {
+      // a masked row's weight is 0, but its registers hold stale words that must not reach the product as NaN/Inf
+      uint32_t va[VEC / 2], vb[VEC / 2];
+      const uint32_t wa[4] = {c.ok[u] ? c.v[u].x : 0u, c.ok[u] ? c.v[u].y : 0u, c.ok[u] ? c.v[u].z : 0u,
                               c.ok[u] ? c.v[u].w : 0u};
+      const uint32_t wb[4] = {c.ok[u + 1] ? c.v[u + 1].x : 0u, c.ok[u + 1] ? c.v[u + 1].y : 0u,
+                              c.ok[u + 1] ? c.v[u + 1].z : 0u, c.ok[u + 1] ? c.v[u + 1].w : 0u};
       if constexpr (!FP8) {
 #pragma unroll
-        for (int w = 0; w < 4; ++w) unpack2<KV_DT>(vw[w], vf[2 * w], vf[2 * w + 1]);
+        for (int w = 0; w < 4; ++w) {
+          va[w] = wa[w];
+          vb[w] = wb[w];
+        }
       } else {
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-          const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(vw[w]), false);
-          const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(vw[w]), true);
-          vf[4 * w + 0] = lo.x;
-          vf[4 * w + 1] = lo.y;
-          vf[4 * w + 2] = hi.x;
-          vf[4 * w + 3] = hi.y;
+          va[2 * w] = e4m3x2_to_16<Q_DT, false>(wa[w]);
+          va[2 * w + 1] = e4m3x2_to_16<Q_DT, true>(wa[w]);
+          vb[2 * w] = e4m3x2_to_16<Q_DT, false>(wb[w]);
+          vb[2 * w + 1] = e4m3x2_to_16<Q_DT, true>(wb[w]);
         }
       }
+      uint32_t pp[G];
 #pragma unroll
       for (int h = 0; h < G; ++h) {
-        const float pu = fast_exp2(s[u][h] - mnew[h]);
-        l[h] += pu;
-        const float pv = FP8 ? (c.ok[u] ? pu * vs[u] : 0.0f) : pu;
+        const float p0 = fast_exp2(s[u][h] - mnew[h]);
+        const float p1 = fast_exp2(s[u + 1][h] - mnew[h]);
+        l[h] += p0;
+        l[h] += p1;
+        const float pv0 = FP8 ? (c.ok[u] ? p0 * vs[u] : 0.0f) : p0;
+        const float pv1 = FP8 ? (c.ok[u + 1] ? p1 * vs[u + 1] : 0.0f) : p1;
+        pp[h] = pack2<Q_DT>(pv0, pv1);
+      }
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) acc[h][i] = fmaf(pv, vf[i], acc[h][i]);
+      for (int j = 0; j < VEC / 2; ++j) {
+        const uint32_t x = __builtin_amdgcn_perm(vb[j], va[j], 0x05040100u);  // element 2j of both tokens
+        const uint32_t y = __builtin_amdgcn_perm(vb[j], va[j], 0x07060302u);  // element 2j + 1
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+          acc[h][2 * j] = dot2<Q_DT>(x, pp[h], acc[h][2 * j]);
+          acc[h][2 * j + 1] = dot2<Q_DT>(y, pp[h], acc[h][2 * j + 1]);
+        }
       }
     }
   };
