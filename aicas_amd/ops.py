@@ -284,10 +284,14 @@ class Workspace:
     """Zero-initialised scratch for split partials and arrival counters, one per (device, stream).
 
     The kernels leave the counters at zero after every launch, so the buffer is reused as is. It only grows;
-    call :meth:`reserve` before capturing a HIP graph so that no allocation happens during capture.
+    call :meth:`reserve` before capturing a HIP graph so that no allocation happens during capture. A buffer
+    that a larger one replaces is kept alive, not freed: a graph captured earlier holds its address and keeps
+    writing partials and counters there on every replay, which must never land in memory the allocator has
+    handed to another tensor.
     """
 
     _pool: dict[tuple[int, int], torch.Tensor] = {}
+    _retired: list[torch.Tensor] = []
 
     @classmethod
     def get(cls, device: torch.device, nbytes: int) -> torch.Tensor:
@@ -298,6 +302,7 @@ class Workspace:
             size = max(nbytes, 1 << 20)
             if buf is not None:
                 size = max(size, 2 * buf.numel())
+                cls._retired.append(buf)
             buf = torch.zeros(size, dtype=torch.uint8, device=device)
             cls._pool[key] = buf
         return buf
@@ -308,7 +313,9 @@ class Workspace:
 
     @classmethod
     def clear(cls) -> None:
+        """Drop every workspace, retired ones included: only when no captured graph still launches on them."""
         cls._pool.clear()
+        cls._retired.clear()
 
 
 def decode_attention(
