@@ -113,6 +113,9 @@ def test_plan_honours_hint_and_rejects_bad_shapes():
     assert _plan(_lib.DTYPE_BF16, 8, 16, 8, 96, 100)[0] == _lib.ERR_UNSUPPORTED
     assert _plan(7, 8, 16, 8, 128, 100)[0] == _lib.ERR_UNSUPPORTED
     assert _plan(_lib.DTYPE_BF16, 0, 16, 8, 128, 100)[0] == _lib.ERR_INVALID
+    # at most 65536 (batch row, kv head) pairs per launch: the workspace's counter region holds that many
+    assert _plan(_lib.DTYPE_BF16, 8192, 16, 8, 128, 32)[0] == _lib.OK
+    assert _plan(_lib.DTYPE_BF16, 8193, 16, 8, 128, 32)[0] == _lib.ERR_UNSUPPORTED
 
 
 FAKE = 0x7F0000000000  # a 16-byte-aligned address that is never dereferenced
