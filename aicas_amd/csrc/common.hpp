@@ -153,6 +153,15 @@ __device__ __forceinline__ float group_max(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// A 16-byte load of data read once per launch (cache rows): non-temporal (global_load_dwordx4 ... nt), so the
+// stream does not allocate in the caches on its way through. The decode kernel's access pattern as a pure read
+// (B=8 L=2112, 69 MB): 12.4 us per launch with these loads, 13.5 with plain ones.
+__device__ __forceinline__ uint4 load_stream16(const void* p) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 w = __builtin_nontemporal_load(static_cast<const u32x4*>(p));
+  return make_uint4(w.x, w.y, w.z, w.w);
+}
+
 // Where a token's K/V row lives. Contiguous caches are the one-block-per-sequence case:
 // block id = batch index, page_size = capacity, and the token stride may be any multiple of 16 bytes.
 struct KVLayout {

@@ -325,8 +325,8 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
         tin = tc & page_mask;
       }
       const int64_t off = blk * p.cache.stride_blk + head_off + static_cast<int64_t>(tin) * p.cache.stride_t;
-      c.k[u] = *reinterpret_cast<const uint4*>(kbase + off * EB + li * 16);
-      c.v[u] = *reinterpret_cast<const uint4*>(vbase + off * EB + li * 16);
+      c.k[u] = load_stream16(kbase + off * EB + li * 16);
+      c.v[u] = load_stream16(vbase + off * EB + li * 16);
       c.ok[u] = ok;
     }
     // fp8: the chunk's scales in one load per lane (not one per row and lane): word j of lane l holds entry
