@@ -94,7 +94,7 @@ __global__ __launch_bounds__(kBlockThreads) void kv_append_kernel(AppendParams p
 #pragma unroll
   for (int k = 0; k < kAppendPasses; ++k) {
     const int r = first_row + k * ROWS_PER_PASS;
-    x[k] = r < rows_total ? *reinterpret_cast<const uint4*>(src_row(r) + lane * VEC) : make_uint4(0u, 0u, 0u, 0u);
+    x[k] = r < rows_total ? load_stream16(src_row(r) + lane * VEC) : make_uint4(0u, 0u, 0u, 0u);
   }
   if (tid == 0) s_pos = p.positions[b];
   __syncthreads();
