@@ -169,11 +169,13 @@ int launch_decode(const aicas::DecodeParams& p, int q_dtype, int kv_dtype, int d
 // launch: B=8 L=2048 (64 (batch, kv head) pairs) 19.4 / 17.1 / 17.4 / 20.7 / 18.4 / 17.4 / 18.2 for 2 / 3 / 4 /
 // 5 / 6 / 7 / 8 splits per pair; B=1 L=32768 (8 pairs) 35.0 / 33.8 / 33.7 / 33.6 / 33.3 / 41.4 / 34.4 / 39.8 for
 // 17 / 20 / 24 / 28 / 31 / 33 / 56 / 65 splits; ragged B=32 paged fp8 (256 pairs) 86.8 / 80.9 / 91.3 for 1 / 2 / 4.
-// With few pairs: about 3/4 of a workgroup per CU and never more than one (a few CUs holding two workgroups
-// make the tail: 264 and 320 workgroups are the slow cases above). With many pairs (batches of ragged
-// lengths): 7/4, so that the longest sequences are split.
-constexpr int kFewPairsWGsPerCUx4 = 3;
-constexpr int kManyPairsWGsPerCUx4 = 7;
+// With few pairs: about 7/8 of a workgroup per CU and never more than one (a few CUs holding two workgroups
+// make the tail: 264 and 320 workgroups are the slow cases above). With the cache rows loaded non-temporal,
+// B=8 L=2048 takes 446.7 us/step at 4 splits against 450.5 at 3, and B=1 L=32768 29.0 / 29.5 / 30.4 / 38.1 us
+// at 24 / 29 / 32 / 33 splits. With many pairs (batches of ragged lengths): 7/4, so that the longest sequences
+// are split. (Both in eighths.)
+constexpr int kFewPairsWGsPerCUx8 = 7;
+constexpr int kManyPairsWGsPerCUx8 = 14;
 
 // Workspace layout. The counters sit at fixed offsets, the same for every launch shape, ahead of the
 // partials: they are zero between launches whatever shapes ran before on the same workspace, since no launch
@@ -210,8 +212,8 @@ int plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int32_t num_kv_he
     // 9.19 us, 9 splits 8.02 us).
     const int64_t pairs = int64_t{batch} * num_kv_heads;
     const int64_t cus = device_cus();
-    const bool few = pairs * 4 <= int64_t{kFewPairsWGsPerCUx4} * cus;
-    const int64_t target = int64_t{few ? kFewPairsWGsPerCUx4 : kManyPairsWGsPerCUx4} * cus / 4;
+    const bool few = pairs * 4 <= 3 * cus;  // at most 3/4 of a pair per CU
+    const int64_t target = int64_t{few ? kFewPairsWGsPerCUx8 : kManyPairsWGsPerCUx8} * cus / 8;
     int64_t splits_wanted = std::max<int64_t>(1, (target + pairs / 2) / pairs);
     if (few) splits_wanted = std::max<int64_t>(1, std::min(splits_wanted, cus / pairs));
     tps = ceil_div(int64_t{max_seq_len > 0 ? max_seq_len : 1}, splits_wanted);
