@@ -18,7 +18,7 @@ import torch  # noqa: F401  (must precede the library load, see above)
 LIB_NAME = "libaicas_decode.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DTYPE_BF16 = 0
 DTYPE_FP16 = 1
@@ -41,6 +41,7 @@ EXPORTED_SYMBOLS = (
     "aicas_decode_plan",
     "aicas_decode_attention",
     "aicas_decode_attention_append",
+    "aicas_decode_attention_append_noalloc",
     "aicas_decode_attention_append_qk",
     "aicas_block_pool_init",
     "aicas_block_alloc",
@@ -149,6 +150,10 @@ def _bind(handle: ctypes.CDLL) -> ctypes.CDLL:
         _I32, _P, _SIZE, _P,
         _P,
     ]
+    handle.aicas_decode_attention_append_noalloc.restype = ctypes.c_int
+    # aicas_decode_attention_append's arguments without (workspace, workspace_bytes)
+    handle.aicas_decode_attention_append_noalloc.argtypes = \
+        handle.aicas_decode_attention_append.argtypes[:-4] + handle.aicas_decode_attention_append.argtypes[-2:]
     handle.aicas_decode_attention_append_qk.restype = ctypes.c_int
     handle.aicas_decode_attention_append_qk.argtypes = [ctypes.POINTER(KVCacheDesc), ctypes.POINTER(QKPrologueDesc)] + \
         handle.aicas_decode_attention_append.argtypes[1:]

@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <cstring>
 #include <algorithm>
+#include <mutex>
 
 #include "aicas_decode.h"
 #include "block_pool.hpp"
@@ -399,6 +400,49 @@ int decode_append(const aicas_kv_cache_t* cache, const aicas_qk_prologue_t* pro,
   return run_decode<true>(c, stream);
 }
 
+// ---------------------------------------------------------------------------------------------------------
+// Scratch of aicas_decode_attention_append_noalloc: the decode workspace (counters, then split partials) as
+// static device memory of the library, one copy per device, held until the process ends. In host code the
+// name `scratch` is only a host-side stand-in: the device address of each device's copy comes from
+// hipGetSymbolAddress, called once per device with that device current, and only that address is ever
+// handed to a kernel.
+constexpr size_t kScratchBytes = size_t{4} << 20;
+static_assert(kScratchBytes > kPartialsOff, "the scratch must hold the counters and some partials");
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Clears n bytes (n a multiple of 16) with vector stores: a kernel rather than hipMemsetAsync, so that a
+// graph capturing the first call records a kernel node.
+__global__ void scratch_clear_kernel(uint4* p, size_t n16) {
+  for (size_t i = blockIdx.x * size_t{blockDim.x} + threadIdx.x; i < n16; i += size_t{gridDim.x} * blockDim.x)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// The current device's scratch address. The first call on a device looks it up and clears the whole array
+// on `stream` (the kernels then keep the counters and partial slots at their between-launch values).
+int scratch_address(hipStream_t stream, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
+    return fail(AICAS_ERR_INVALID, "no usable current HIP device (got %d)", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(AICAS_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+    hipLaunchKernelGGL(scratch_clear_kernel, dim3(256), dim3(256), 0, stream, static_cast<uint4*>(ptr),
+                       kScratchBytes / 16);
+    const int rc = check_launch("aicas_decode_attention_append_noalloc (scratch clear)");
+    if (rc) return rc;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return AICAS_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -507,6 +551,34 @@ int aicas_decode_attention_append(const aicas_kv_cache_t* cache, int32_t q_dtype
                        v_stride_b, v_stride_h, out, out_stride_b, out_stride_h, positions, seq_lens_out, min_len,
                        max_seq_len, batch, num_q_heads, num_kv_heads, head_dim, sm_scale, tokens_per_split, workspace,
                        workspace_bytes, status, stream);
+}
+
+int aicas_decode_attention_append_noalloc(const aicas_kv_cache_t* cache, int32_t q_dtype, const void* q,
+                                          int64_t q_stride_b, int64_t q_stride_h, const void* k_new,
+                                          int64_t k_stride_b, int64_t k_stride_h, const void* v_new,
+                                          int64_t v_stride_b, int64_t v_stride_h, void* out, int64_t out_stride_b,
+                                          int64_t out_stride_h, const int32_t* positions, int32_t* seq_lens_out,
+                                          int32_t min_len, int32_t max_seq_len, int32_t batch, int32_t num_q_heads,
+                                          int32_t num_kv_heads, int32_t head_dim, float sm_scale,
+                                          int32_t tokens_per_split, int32_t* status, hipStream_t stream) {
+  // the launch's workspace size, checked against the scratch before anything touches the device
+  if (!cache) return fail(AICAS_ERR_INVALID, "cache descriptor is NULL");
+  Plan pl{};
+  int rc = plan(cache->kv_dtype, batch, num_q_heads, num_kv_heads, head_dim, max_seq_len,
+                cache->block_table ? cache->page_size : 0, tokens_per_split, pl);
+  if (rc) return rc;
+  if (pl.bytes > kScratchBytes)
+    return fail(AICAS_ERR_WORKSPACE,
+                "this launch needs a %zu-byte workspace; the library's static scratch holds %zu bytes "
+                "(use aicas_decode_attention_append with a caller-allocated workspace)",
+                pl.bytes, kScratchBytes);
+  void* ws = nullptr;
+  rc = scratch_address(stream, &ws);
+  if (rc) return rc;
+  return decode_append(cache, nullptr, q_dtype, q, q_stride_b, q_stride_h, k_new, k_stride_b, k_stride_h, v_new,
+                       v_stride_b, v_stride_h, out, out_stride_b, out_stride_h, positions, seq_lens_out, min_len,
+                       max_seq_len, batch, num_q_heads, num_kv_heads, head_dim, sm_scale, tokens_per_split, ws,
+                       kScratchBytes, status, stream);
 }
 
 int aicas_decode_attention_append_qk(const aicas_kv_cache_t* cache, const aicas_qk_prologue_t* prologue,

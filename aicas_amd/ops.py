@@ -422,6 +422,48 @@ class QKPrologue:
         return [t for t in (self.q_norm_weight, self.k_norm_weight, self.cos, self.sin, self.q_out) if t is not None]
 
 
+def _append_call(q, cache, k_new, v_new, positions, *, sm_scale, max_seq_len, min_seq_len, seq_lens_out, out,
+                 tokens_per_split, status, extra=()):
+    """Checks shared by the fused append + attend entry points; returns the output tensor, the plan, the cache
+    descriptor and the C-ABI arguments that follow it up to tokens_per_split, and the trailing (status,
+    stream)."""
+    squeeze = q.dim() == 3
+    q4 = q.unsqueeze(2) if squeeze else q
+    if q4.dim() != 4 or q4.shape[2] != 1 or q4.stride(3) != 1:
+        raise AicasError(_lib.ERR_INVALID, "q must be [B, Hq, 1, D] with unit head_dim stride")
+    B, Hq, _, D = q4.shape
+    kn = k_new.squeeze(2) if k_new.dim() == 4 else k_new
+    vn = v_new.squeeze(2) if v_new.dim() == 4 else v_new
+    if kn.shape != (B, cache.num_kv_heads, D) or vn.shape != kn.shape or kn.stride(2) != 1 or vn.stride(2) != 1:
+        raise AicasError(_lib.ERR_INVALID, "k_new/v_new must be [B, Hkv, 1, D] with unit head_dim stride")
+    if kn.dtype != q.dtype or vn.dtype != q.dtype:
+        raise AicasError(_lib.ERR_INVALID, "k_new/v_new must have q's dtype")
+    if D != cache.head_dim:
+        raise AicasError(_lib.ERR_INVALID, f"q head_dim {D} != cache head_dim {cache.head_dim}")
+    if positions.dtype != torch.int32 or positions.numel() < B or not positions.is_contiguous():
+        raise AicasError(_lib.ERR_INVALID, "positions must be a contiguous int32 tensor with one entry per sequence")
+    if seq_lens_out is not None and (seq_lens_out.dtype != torch.int32 or not seq_lens_out.is_contiguous()):
+        raise AicasError(_lib.ERR_INVALID, "seq_lens_out must be a contiguous int32 tensor")
+    _require_gpu(cache.k, q4, kn, vn, positions, seq_lens_out, out, status, *extra)
+    if out is None:
+        out = torch.empty((B, Hq, 1, D), dtype=q.dtype, device=q.device)
+    out4 = out.unsqueeze(2) if out.dim() == 3 else out
+    if out4.shape != (B, Hq, 1, D) or out4.stride(3) != 1 or out4.dtype != q.dtype:
+        raise AicasError(_lib.ERR_INVALID, "out must be [B, Hq, 1, D] in q's dtype with unit head_dim stride")
+    pl = decode_plan(
+        cache.k.dtype, B, Hq, cache.num_kv_heads, D, max_seq_len, cache.page_size if cache.paged else 0,
+        tokens_per_split,
+    )
+    desc = cache.desc()
+    head = (dtype_code(q.dtype), q4.data_ptr(), q4.stride(0), q4.stride(1),
+            kn.data_ptr(), kn.stride(0), kn.stride(1), vn.data_ptr(), vn.stride(0), vn.stride(1),
+            out4.data_ptr(), out4.stride(0), out4.stride(1),
+            positions.data_ptr(), _ptr(seq_lens_out), int(min_seq_len), int(max_seq_len),
+            B, Hq, cache.num_kv_heads, D, float(sm_scale), pl.tokens_per_split)
+    tail = (_ptr(status), _stream(cache.device))
+    return out, pl, desc, head, tail
+
+
 def decode_attention_append(
     q: torch.Tensor,
     cache: KVCacheView,
@@ -445,47 +487,50 @@ def decode_attention_append(
     lower bound on every ``positions[b]``, used as by :func:`decode_attention`. With ``qk``, q and ``k_new`` are
     the projections' outputs and are normalised and rotated as the model does before use
     (``aicas_decode_attention_append_qk``)."""
-    squeeze = q.dim() == 3
-    q4 = q.unsqueeze(2) if squeeze else q
-    if q4.dim() != 4 or q4.shape[2] != 1 or q4.stride(3) != 1:
-        raise AicasError(_lib.ERR_INVALID, "q must be [B, Hq, 1, D] with unit head_dim stride")
-    B, Hq, _, D = q4.shape
-    kn = k_new.squeeze(2) if k_new.dim() == 4 else k_new
-    vn = v_new.squeeze(2) if v_new.dim() == 4 else v_new
-    if kn.shape != (B, cache.num_kv_heads, D) or vn.shape != kn.shape or kn.stride(2) != 1 or vn.stride(2) != 1:
-        raise AicasError(_lib.ERR_INVALID, "k_new/v_new must be [B, Hkv, 1, D] with unit head_dim stride")
-    if kn.dtype != q.dtype or vn.dtype != q.dtype:
-        raise AicasError(_lib.ERR_INVALID, "k_new/v_new must have q's dtype")
-    if D != cache.head_dim:
-        raise AicasError(_lib.ERR_INVALID, f"q head_dim {D} != cache head_dim {cache.head_dim}")
-    if positions.dtype != torch.int32 or positions.numel() < B or not positions.is_contiguous():
-        raise AicasError(_lib.ERR_INVALID, "positions must be a contiguous int32 tensor with one entry per sequence")
-    if seq_lens_out is not None and (seq_lens_out.dtype != torch.int32 or not seq_lens_out.is_contiguous()):
-        raise AicasError(_lib.ERR_INVALID, "seq_lens_out must be a contiguous int32 tensor")
-    _require_gpu(cache.k, q4, kn, vn, positions, seq_lens_out, out, workspace, status,
-                 *(qk.tensors() if qk is not None else ()))
-    if out is None:
-        out = torch.empty((B, Hq, 1, D), dtype=q.dtype, device=q.device)
-    out4 = out.unsqueeze(2) if out.dim() == 3 else out
-    if out4.shape != (B, Hq, 1, D) or out4.stride(3) != 1 or out4.dtype != q.dtype:
-        raise AicasError(_lib.ERR_INVALID, "out must be [B, Hq, 1, D] in q's dtype with unit head_dim stride")
-    pl = decode_plan(
-        cache.k.dtype, B, Hq, cache.num_kv_heads, D, max_seq_len, cache.page_size if cache.paged else 0,
-        tokens_per_split,
-    )
+    extra = (workspace, *(qk.tensors() if qk is not None else ()))
+    out, pl, desc, head, tail = _append_call(
+        q, cache, k_new, v_new, positions, sm_scale=sm_scale, max_seq_len=max_seq_len, min_seq_len=min_seq_len,
+        seq_lens_out=seq_lens_out, out=out, tokens_per_split=tokens_per_split, status=status, extra=extra)
     if workspace is None:
         workspace = Workspace.get(cache.device, pl.workspace_bytes)
-    desc = cache.desc()
-    args = (dtype_code(q.dtype), q4.data_ptr(), q4.stride(0), q4.stride(1),
-            kn.data_ptr(), kn.stride(0), kn.stride(1), vn.data_ptr(), vn.stride(0), vn.stride(1),
-            out4.data_ptr(), out4.stride(0), out4.stride(1),
-            positions.data_ptr(), _ptr(seq_lens_out), int(min_seq_len), int(max_seq_len),
-            B, Hq, cache.num_kv_heads, D, float(sm_scale),
-            pl.tokens_per_split, workspace.data_ptr(), workspace.numel(), _ptr(status),
-            _stream(cache.device))
+    args = (*head, workspace.data_ptr(), workspace.numel(), *tail)
     if qk is None:
         check(_lib.lib().aicas_decode_attention_append(ctypes.byref(desc), *args))
     else:
+        B, Hq, D = out.shape[0], out.shape[1], out.shape[-1]
         pro = qk.desc(B, Hq, D, q.dtype)
         check(_lib.lib().aicas_decode_attention_append_qk(ctypes.byref(desc), ctypes.byref(pro), *args))
+    return out
+
+
+# Bytes of the library's static scratch behind aicas_decode_attention_append_noalloc.
+NOALLOC_SCRATCH_BYTES = 4 << 20
+
+
+def decode_attention_append_noalloc(
+    q: torch.Tensor,
+    cache: KVCacheView,
+    k_new: torch.Tensor,
+    v_new: torch.Tensor,
+    positions: torch.Tensor,
+    *,
+    out: torch.Tensor,
+    sm_scale: float,
+    max_seq_len: int,
+    min_seq_len: int = 0,
+    seq_lens_out: torch.Tensor | None = None,
+    tokens_per_split: int = 0,
+    status: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """:func:`decode_attention_append` for callers that cannot allocate: ``out`` must be given, and the split
+    partials live in the library's static per-device scratch (``aicas_decode_attention_append_noalloc``), so
+    neither this function nor the library allocates device memory. Launches whose workspace would exceed
+    ``NOALLOC_SCRATCH_BYTES`` raise ``AicasError`` (ERR_WORKSPACE). Calls that may overlap on one device share
+    the scratch and must be serialised by the caller."""
+    if out is None:
+        raise AicasError(_lib.ERR_INVALID, "decode_attention_append_noalloc needs a preallocated out")
+    out, _, desc, head, tail = _append_call(
+        q, cache, k_new, v_new, positions, sm_scale=sm_scale, max_seq_len=max_seq_len, min_seq_len=min_seq_len,
+        seq_lens_out=seq_lens_out, out=out, tokens_per_split=tokens_per_split, status=status)
+    check(_lib.lib().aicas_decode_attention_append_noalloc(ctypes.byref(desc), *head, *tail))
     return out

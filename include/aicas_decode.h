@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define AICAS_ABI_VERSION 5
+#define AICAS_ABI_VERSION 6
 
 /* Element types. */
 #define AICAS_DTYPE_BF16 0
@@ -156,6 +156,26 @@ int aicas_decode_attention_append(const aicas_kv_cache_t* cache, int32_t q_dtype
                                   int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, float sm_scale,
                                   int32_t tokens_per_split, void* workspace, size_t workspace_bytes, int32_t* status,
                                   hipStream_t stream);
+
+/*
+ * aicas_decode_attention_append without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. Same arguments, results and status bits as aicas_decode_attention_append; the split partials and
+ * counters live in a 4 MiB static scratch array of the library, one per device, which each device holds until
+ * the process ends. The entry point calls no allocator. A launch whose workspace (aicas_decode_plan's
+ * workspace_bytes) exceeds 4 MiB is rejected with AICAS_ERR_WORKSPACE before anything is enqueued. Every call
+ * on a device shares that device's scratch: calls that may overlap on one device (two streams, or two host
+ * threads) race and must be serialised by the caller. The first call on a device also enqueues, on `stream`,
+ * one small kernel that clears the scratch.
+ */
+int aicas_decode_attention_append_noalloc(const aicas_kv_cache_t* cache, int32_t q_dtype, const void* q,
+                                          int64_t q_stride_b, int64_t q_stride_h, const void* k_new,
+                                          int64_t k_stride_b, int64_t k_stride_h, const void* v_new,
+                                          int64_t v_stride_b, int64_t v_stride_h, void* out, int64_t out_stride_b,
+                                          int64_t out_stride_h, const int32_t* positions, int32_t* seq_lens_out,
+                                          int32_t min_len, int32_t max_seq_len, int32_t batch, int32_t num_q_heads,
+                                          int32_t num_kv_heads, int32_t head_dim, float sm_scale,
+                                          int32_t tokens_per_split, int32_t* status, hipStream_t stream);
 
 /*
  * The model's q/k preparation, fused into aicas_decode_attention_append_qk. Every pointer may be NULL (that
