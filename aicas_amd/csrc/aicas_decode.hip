@@ -25,6 +25,7 @@ namespace {
 
 thread_local char g_last_error[512] = "";
 
+
 int fail(int code, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -45,6 +46,18 @@ int check_launch(const char* what) {
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Byte range [lo, hi) spanned by a [n0, n1, d] 16-bit tensor with element strides s0, s1 (non-negative) and a
+// unit last stride.
+struct Extent {
+  uintptr_t lo, hi;
+};
+Extent extent16(const void* p, int64_t n0, int64_t s0, int64_t n1, int64_t s1, int64_t d) {
+  const uintptr_t lo = reinterpret_cast<uintptr_t>(p);
+  const int64_t last = (n0 - 1) * s0 + (n1 - 1) * s1 + d;
+  return {lo, lo + static_cast<uintptr_t>(std::max<int64_t>(last, 0)) * 2};
+}
+bool overlaps(const Extent& a, const Extent& b) { return a.lo < b.hi && b.lo < a.hi; }
 bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 int ilog2(int64_t x) {
   int s = 0;
@@ -334,6 +347,17 @@ int run_decode(const DecodeCall& c, hipStream_t stream) {
       return fail(AICAS_ERR_INVALID, "cos/sin rows must be 16-byte aligned with strides that are multiples of 8");
     if (pro.q_out && (!aligned16(pro.q_out) || (pro.q_out_stride_b % 8) || (pro.q_out_stride_h % 8)))
       return fail(AICAS_ERR_INVALID, "q_out must be 16-byte aligned with strides that are multiples of 8");
+    if (pro.q_out) {
+      // q_out is written once every workgroup of its (batch row, kv head) has read q and the new rows: it may
+      // be q itself, but no other overlap with q or with k_new is allowed
+      const Extent qo = extent16(pro.q_out, c.batch, pro.q_out_stride_b, c.num_q_heads, pro.q_out_stride_h,
+                                 c.head_dim);
+      const Extent qi = extent16(c.q, c.batch, c.q_stride_b, c.num_q_heads, c.q_stride_h, c.head_dim);
+      const Extent kn = extent16(c.k_new, c.batch, c.kn_stride_b, c.num_kv_heads, c.kn_stride_h, c.head_dim);
+      const bool same_as_q = pro.q_out == c.q && pro.q_out_stride_b == c.q_stride_b && pro.q_out_stride_h == c.q_stride_h;
+      if ((!same_as_q && overlaps(qo, qi)) || overlaps(qo, kn))
+        return fail(AICAS_ERR_INVALID, "q_out may be q itself but must not otherwise overlap q or k_new");
+    }
     p.q_norm_w = pro.q_norm_weight;
     p.k_norm_w = pro.k_norm_weight;
     p.norm_eps = pro.eps;

@@ -39,12 +39,12 @@
 //
 // Fused append (APPEND): positions[b] is the length before this step; the kernel attends over
 // L_b = positions[b] + 1 tokens, of which token L_b - 1 comes from the new rows (k_new / v_new) instead of the
-// cache: every workgroup stages the rows in LDS and the wave that streams the token swaps them in before
+// cache: every workgroup stages the rows in LDS and the wave that streams the token selects them in before
 // consuming its chunk, and split 0 writes the row into the cache (quantized on write for fp8 caches, with the
 // attention then using the dequantised row, exactly what a separate append followed by attention would read).
-// Every workgroup of batch row b counts itself in when it exits (it read positions[b] at the start); the last
-// one to do so stores positions[b] + 1 to seq_lens_out[b] (which may alias positions), so no workgroup can read
-// a bumped length.
+// Every workgroup of batch row b counts itself in once all its waves have read positions[b]; the last one to do
+// so stores positions[b] + 1 to seq_lens_out[b] (which may alias positions) as it exits, so no workgroup can
+// read a bumped length.
 #pragma once
 
 #include "common.hpp"
@@ -367,9 +367,9 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
     load_rows(ca, spec_t0, p.cache.max_tokens, -1, 0, true, 0);
     load_rows(cb, spec_t0 + CW, p.cache.max_tokens, -1, 0, true, 0);
   }
-  // APPEND with seq_lens_out: every workgroup counts itself in on its way out (each of its waves' reads of
-  // positions[b] completed long before: every wave used the value to plan its work); the last of the batch
-  // row's workgroups stores the bumped length, so no workgroup can read it. Counting in at exit keeps the
+  // APPEND with seq_lens_out: every workgroup counts itself in on its way out, after a barrier that each of its
+  // waves passes once it has read positions[b] (every wave used the value to plan its work); the last of the
+  // batch row's workgroups stores the bumped length, so no workgroup can read it. Counting in at exit keeps the
   // contended atomic off the start of the stream.
   auto count_in = [&]() {
     if constexpr (APPEND) {
@@ -401,6 +401,7 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   }
   const int n_active = L > 0 ? (L + tps - 1) / tps : 1;
   if (split >= n_active) {
+    __syncthreads();  // every wave has read positions[b]
     count_in();
     return;
   }
@@ -605,7 +606,8 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   auto prologue_work = [&]() {
     // QK: q and the new K row as the model prepares them, one pair per thread and round (their loads were
     // issued before every load of the cache, so waiting for them leaves the first super-chunk in flight), into
-    // LDS; split 0 also writes the prepared q to q_out. Then every lane takes its q slices from there.
+    // LDS (the workgroup that writes the output also writes the prepared q to q_out from there). Then every
+    // lane takes its q slices from there.
     if constexpr (QK) {
 #pragma unroll
       for (int i = 0; i < kQKRounds; ++i) {
@@ -616,14 +618,7 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
         unpack2<Q_DT>(qk_x[i], x0, x1);
         qk_pair<Q_DT, D>(x0, x1, d0, qk_w[i], r < G ? qk_norm_q : qk_norm_k, qk_c[i], qk_s[i], qk_rope,
                          p.norm_eps);
-        const uint32_t packed = pack2<Q_DT>(x0, x1);
-        if (pp < kQKPairs) {
-          s_qk[pp] = packed;
-          if (r < G && p.q_out && split == 0) {
-            *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.q_out) + b * p.q_out_stride_b +
-                                         (kvh * G + r) * p.q_out_stride_h + d0) = packed;
-          }
-        }
+        if (pp < kQKPairs) s_qk[pp] = pack2<Q_DT>(x0, x1);
       }
       __syncthreads();
 #pragma unroll
@@ -704,31 +699,38 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   prologue_work();
   if constexpr (APPEND) __syncthreads();  // the staged new rows are visible to every wave
 
-  // APPEND: token t_new of a chunk (skipped when the chunk was loaded) comes from the staged new rows, swapped
-  // in just before the chunk is consumed, when its loads have landed anyway (only the chunk holding it takes
-  // this branch). The token is thus attended to at its place in the stream, exactly as a separate append
-  // followed by attention would.
-  auto take_new_row = [&](ChunkT& c, int t0) {
+  // APPEND: token t_new of a chunk (masked when the chunk was loaded) comes from the staged new rows, selected
+  // into a copy of the chunk just before it is consumed, when its loads have landed anyway (only the chunk
+  // holding it takes this branch). The token is thus attended to at its place in the stream, exactly as a
+  // separate append followed by attention would. The buffer itself is never written here: overwriting it in
+  // place (a second definition of the loop-carried registers) made the compiler copy both buffers at the loop
+  // head on every round, each copy waiting for its loads, down to vmcnt(0), in the variants without SPEC.
+  auto consume_chunk = [&](const ChunkT& c, int t0) {
     if constexpr (APPEND) {
       if (t_new >= t0 && t_new < t0 + CW) {
+        ChunkT cs = c;
+        const uint4 nk = s_new[li];
+        const uint4 nv = s_new[R + li];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          if (t0 + u * RPW + row == t_new) {
-            c.k[u] = s_new[li];
-            c.v[u] = s_new[R + li];
-            c.ok[u] = true;
-          }
+          const bool isn = t0 + u * RPW + row == t_new;
+          cs.k[u] = isn ? nk : c.k[u];
+          cs.v[u] = isn ? nv : c.v[u];
+          cs.ok[u] = isn || c.ok[u];
         }
         if constexpr (FP8) {
-          const int ik = t_new - t0;  // its K scale is entry ik of the chunk's scales, its V scale NS + ik
+          const int ik = t_new - t0;
 #pragma unroll
           for (int j = 0; j < NSW; ++j) {
-            if (j * kWave + lane == ik) c.sc[j] = s_new_scale[0];
-            if (j * kWave + lane == NS + ik) c.sc[j] = s_new_scale[1];
+            if (j * kWave + lane == ik) cs.sc[j] = s_new_scale[0];
+            if (j * kWave + lane == NS + ik) cs.sc[j] = s_new_scale[1];
           }
         }
+        consume(cs);
+        return;
       }
     }
+    consume(c);
   };
   // first token of the chunk each buffer holds (far below 0 for a dummy, which holds none)
   int ca_t0 = sc0 >= 0 ? sc0 : -(1 << 30);
@@ -753,23 +755,19 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   };
   int k = 0;  // super-chunks of this wave taken so far
   for (int nsc = super_start(++k); nsc >= 0; nsc = super_start(++k)) {
-    take_new_row(ca, ca_t0);
-    consume(ca);
+    consume_chunk(ca, ca_t0);
     settle();
     load_chunk(ca, nsc, true);
     ca_t0 = nsc;
     __builtin_amdgcn_sched_barrier(0);
-    take_new_row(cb, cb_t0);
-    consume(cb);
+    consume_chunk(cb, cb_t0);
     settle();
     load_chunk(cb, nsc + CW, true);
     cb_t0 = nsc + CW;
     __builtin_amdgcn_sched_barrier(0);
   }
-  take_new_row(ca, ca_t0);
-  consume(ca);
-  take_new_row(cb, cb_t0);
-  consume(cb);
+  consume_chunk(ca, ca_t0);
+  consume_chunk(cb, cb_t0);
 
   // Merge the row groups of this wave (lanes li, li + R, li + 2R, ... hold the same head_dim slice).
 #pragma unroll
@@ -803,10 +801,12 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   }
   __syncthreads();
 
-  // Merge the 4 waves; either finish the output (one split) or publish this split's partial state.
-  const bool single = (n_active == 1);
-  uint16_t* outb = static_cast<uint16_t*>(p.out) + b * p.out_stride_b;
-  for (int idx = tid; idx < G * D; idx += kBlockThreads) {
+  // Merge the 4 waves into this split's partial state (m, l, acc), one (head, d) cell per thread and round.
+  constexpr int CPT = (G * D + kBlockThreads - 1) / kBlockThreads;
+  float pm[CPT], pl[CPT], pa[CPT];
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int idx = min(tid + c * kBlockThreads, G * D - 1);
     const int h = idx / D;
     const int d = idx % D;
     float M = s_m[0][h];
@@ -815,31 +815,63 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
     float ls = 0.0f, a = 0.0f;
 #pragma unroll
     for (int w = 0; w < kWavesPerBlock; ++w) {
-      const float c = fast_exp2(s_m[w][h] - M);
-      ls = fmaf(s_l[w][h], c, ls);
-      a = fmaf(s_acc[w][h][d], c, a);
+      const float cw = fast_exp2(s_m[w][h] - M);
+      ls = fmaf(s_l[w][h], cw, ls);
+      a = fmaf(s_acc[w][h][d], cw, a);
     }
-    const int hq = kvh * G + h;
-    if (single) {
-      outb[hq * p.out_stride_h + d] = from_f32<Q_DT>(ls > 0.0f ? a / ls : 0.0f);
-    } else {
-      const int64_t pidx = (static_cast<int64_t>(b) * p.num_q_heads + hq) * p.max_splits + split;
-      store_agent(p.ws_acc + pidx * D + d, a);
-      if (d == 0) {
-        store_agent(p.ws_ml + 2 * pidx, M);
-        store_agent(p.ws_ml + 2 * pidx + 1, ls);
+    pm[c] = M;
+    pl[c] = ls;
+    pa[c] = a;
+  }
+
+  uint16_t* outb = static_cast<uint16_t*>(p.out) + b * p.out_stride_b;
+  auto write_out = [&](const float* ls, const float* a) {
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int idx = tid + c * kBlockThreads;
+      if (idx < G * D) {
+        const int hq = kvh * G + idx / D;
+        outb[hq * p.out_stride_h + idx % D] = from_f32<Q_DT>(ls[c] > 0.0f ? a[c] / ls[c] : 0.0f);
       }
     }
-  }
-  if (single) {
+    // QK: the prepared q goes out from the workgroup that writes the output, after every split of the pair has
+    // read q (q_out may be q itself)
+    if constexpr (QK) {
+      if (p.q_out) {
+        for (int pp = tid; pp < G * (D / 2); pp += kBlockThreads) {
+          *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.q_out) + b * p.q_out_stride_b +
+                                       (kvh * G + pp / (D / 2)) * p.q_out_stride_h + 2 * (pp % (D / 2))) = s_qk[pp];
+        }
+      }
+    }
+  };
+  if (n_active == 1) {
+    write_out(pl, pa);
     count_in();
     return;
   }
 
-  // Arrival: the partial stores above are complete (device-visible) before the counter moves.
+  // Publish this split's partial with agent-scope stores, wait until they have completed (vmcnt(0): on gfx950
+  // an agent-scope store writes through to the device coherence point and is acknowledged from there), then
+  // count in on the pair's arrival counter. The split that arrives last reads every split's partial with
+  // agent-scope loads (which miss in the non-coherent caches and read that same point), combines them and
+  // re-arms the counter. No workgroup ever waits for another.
+  const int64_t pair_base = (static_cast<int64_t>(b) * p.num_q_heads + kvh * G) * p.max_splits;  // head h: + h * max_splits
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int idx = tid + c * kBlockThreads;
+    if (idx < G * D) {
+      const int64_t pidx = pair_base + (idx / D) * p.max_splits + split;
+      store_agent(p.ws_acc + pidx * D + idx % D, pa[c]);
+      if (idx % D == 0) {
+        store_agent(p.ws_ml + 2 * pidx, pm[c]);
+        store_agent(p.ws_ml + 2 * pidx + 1, pl[c]);
+      }
+    }
+  }
   wait_vmem();
   __syncthreads();
-  int32_t* counter = p.ws_counter + static_cast<int64_t>(b) * p.num_kv_heads + kvh;
+  int32_t* const counter = p.ws_counter + static_cast<int64_t>(b) * p.num_kv_heads + kvh;
   if (tid == 0) {
     const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = (prev == n_active - 1) ? 1 : 0;
@@ -850,23 +882,26 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
     return;
   }
 
-  // One online pass over the splits, MB at a time: the MB partials' loads are independent and in flight
-  // together, so the merge costs about n_active / MB memory round trips.
+  // One online pass over the splits in order, MB at a time: the MB partials' loads are issued unconditionally
+  // (past the last split they repeat it, masked below), so they are in flight together and the merge costs
+  // about n_active / MB memory round trips; loads behind per-split branches would each end in a wait of their
+  // own.
   constexpr int MB = 8;
-  for (int idx = tid; idx < G * D; idx += kBlockThreads) {
-    const int h = idx / D;
+  float rl[CPT], ra[CPT];
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int idx = min(tid + c * kBlockThreads, G * D - 1);
+    const int64_t hbase = pair_base + (idx / D) * p.max_splits;
     const int d = idx % D;
-    const int hq = kvh * G + h;
-    const int64_t base = (static_cast<int64_t>(b) * p.num_q_heads + hq) * p.max_splits;
     float M = kNegBig, ls = 0.0f, a = 0.0f;
     for (int i0 = 0; i0 < n_active; i0 += MB) {
       float mi[MB], li[MB], ai[MB];
 #pragma unroll
       for (int j = 0; j < MB; ++j) {
-        const int i = min(i0 + j, n_active - 1);  // duplicates of the last split are masked below
-        mi[j] = load_agent(p.ws_ml + 2 * (base + i));
-        li[j] = load_agent(p.ws_ml + 2 * (base + i) + 1);
-        ai[j] = load_agent(p.ws_acc + (base + i) * D + d);
+        const int i = min(i0 + j, n_active - 1);
+        mi[j] = load_agent(p.ws_ml + 2 * (hbase + i));
+        li[j] = load_agent(p.ws_ml + 2 * (hbase + i) + 1);
+        ai[j] = load_agent(p.ws_acc + (hbase + i) * D + d);
       }
 #pragma unroll
       for (int j = 0; j < MB; ++j) {
@@ -880,8 +915,10 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
         }
       }
     }
-    outb[hq * p.out_stride_h + d] = from_f32<Q_DT>(ls > 0.0f ? a / ls : 0.0f);
+    rl[c] = ls;
+    ra[c] = a;
   }
+  write_out(rl, ra);
   if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   count_in();
 }

@@ -186,7 +186,8 @@ int aicas_decode_attention_append_noalloc(const aicas_kv_cache_t* cache, int32_t
  *                                 of 8): rotary embedding x * cos + rotate_half(x) * sin, rotate_half(x) =
  *                                 (-x[D/2:], x[:D/2]), each product and the sum rounded to q_dtype;
  *   q_out                         [B, Hq, head_dim] (strides in elements, multiples of 8): receives q as
- *                                 prepared.
+ *                                 prepared, once every workgroup has read q; it may be q itself (same
+ *                                 pointer and strides), but may not otherwise overlap q or k_new.
  * Pointers are 16-byte aligned.
  */
 typedef struct aicas_qk_prologue {
