@@ -201,8 +201,9 @@ constexpr size_t kBatchArriveOff = kCounterBytes;  // [batch] readers of positio
 constexpr size_t kPartialsOff = 2 * kCounterBytes;
 
 struct Plan {
-  int32_t tokens_per_split;
+  int32_t tokens_per_split;  // a sequence of L tokens takes min(num_splits, ceil(L / tokens_per_split)) splits
   int32_t num_splits;
+  int32_t len_limit;  // longest sequence the launch can attend in full (paged caches: LDS block-id cache)
   size_t ml_off, acc_off, bytes;
 };
 
@@ -217,9 +218,15 @@ int plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int32_t num_kv_he
                 (long long)kMaxPairs);
   const int tpi = tokens_per_iteration(kv_dtype, head_dim);
   const int rpb = rows_per_load(kv_dtype, head_dim);
-  int64_t tps;
+  const int64_t bound = max_seq_len > 0 ? max_seq_len : 1;
+  // A split streaming a static range (paged rows too long for the LDS block-id cache) may touch at most
+  // kMaxBlockEntries block-table entries: at most `cap` tokens per split.
+  const int64_t cap = page_size > 0 ? (int64_t{aicas::kMaxBlockEntries} - 2) * page_size / tpi * tpi : 0;
+  int64_t tps, splits;
   if (hint > 0) {
     tps = ceil_div(hint, rpb) * rpb;
+    if (cap >= tpi && tps > cap) tps = cap;
+    splits = ceil_div(bound, tps);
   } else {
     // Split count: the workgroups per compute unit above, in total. A split covers at least one super-chunk
     // (two chunks) per wave: below that its merge costs more than its streaming saves (B=1 L=1024: 17 splits
@@ -229,21 +236,30 @@ int plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int32_t num_kv_he
     const bool few = pairs * 4 <= 3 * cus;  // at most 3/4 of a pair per CU
     const int64_t target = int64_t{few ? kFewPairsWGsPerCUx8 : kManyPairsWGsPerCUx8} * cus / 8;
     int64_t splits_wanted = std::max<int64_t>(1, (target + pairs / 2) / pairs);
-    if (few) splits_wanted = std::max<int64_t>(1, std::min(splits_wanted, cus / pairs));
-    tps = ceil_div(int64_t{max_seq_len > 0 ? max_seq_len : 1}, splits_wanted);
-    tps = ceil_div(tps, rpb) * rpb;
-    if (tps < 2 * tpi) tps = 2 * tpi;
-  }
-  // A split streaming a static range may touch at most kMaxBlockEntries block-table entries.
-  if (page_size > 0) {
-    const int64_t cap = (int64_t{aicas::kMaxBlockEntries} - 2) * page_size / tpi * tpi;
-    if (cap >= tpi && tps > cap) tps = cap;
+    if (few) {
+      // Few pairs (uniform batches, one long sequence): every sequence long enough is spread over the same
+      // number of splits whatever the bound, and each takes min(splits, ceil(L / minimum split)) from its own
+      // length: a launch sized for a loose bound (a graph captured at the cache capacity) runs the grid a tight
+      // bound would give.
+      splits_wanted = std::max<int64_t>(1, std::min(splits_wanted, cus / pairs));
+      tps = 2 * tpi;
+      splits = std::min(splits_wanted, ceil_div(bound, tps));
+      if (cap >= tpi) splits = std::max(splits, ceil_div(bound, cap));
+    } else {
+      // Many pairs (ragged batches): splits in proportion to the length, so that the longest sequences split.
+      tps = ceil_div(bound, splits_wanted);
+      tps = ceil_div(tps, rpb) * rpb;
+      if (tps < 2 * tpi) tps = 2 * tpi;
+      if (cap >= tpi && tps > cap) tps = cap;
+      splits = ceil_div(bound, tps);
+    }
   }
   if (tps > (int64_t{1} << 30)) tps = int64_t{1} << 30;
-  const int64_t splits = max_seq_len > 0 ? ceil_div(max_seq_len, tps) : 1;
   if (splits > 65535) return fail(AICAS_ERR_UNSUPPORTED, "too many splits (%lld)", (long long)splits);
   pl.tokens_per_split = static_cast<int32_t>(tps);
   pl.num_splits = static_cast<int32_t>(splits);
+  const int64_t lim = cap >= tpi ? cap * splits : int64_t{INT32_MAX};
+  pl.len_limit = static_cast<int32_t>(std::min<int64_t>(lim, INT32_MAX));
   const size_t parts = size_t(batch) * num_q_heads * splits;
   pl.ml_off = kPartialsOff;
   pl.acc_off = pl.ml_off + align_up(parts * 2 * sizeof(float), 256);
@@ -313,6 +329,7 @@ int run_decode(const DecodeCall& c, hipStream_t stream) {
   p.num_kv_heads = c.num_kv_heads;
   p.tokens_per_split = pl.tokens_per_split;
   p.max_splits = pl.num_splits;
+  p.len_limit = pl.len_limit;
   // Splits that every sequence keeps busy by the caller's lower bound: they may fetch their first rows before
   // reading the length. A wrong bound only costs bandwidth: the rows' validity always comes from the length.
   p.spec_splits = c.min_attended > 0

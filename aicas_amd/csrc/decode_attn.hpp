@@ -61,8 +61,9 @@ struct DecodeParams {
   int32_t uniform_len;
   int32_t num_q_heads;
   int32_t num_kv_heads;
-  int32_t tokens_per_split;
+  int32_t tokens_per_split;  // a sequence of L tokens takes min(max_splits, ceil(L / tokens_per_split)) splits
   int32_t max_splits;  // == gridDim.x
+  int32_t len_limit;   // longest sequence a launch attends in full (with the cache capacity)
   int32_t spec_splits; // splits every sequence keeps busy by the caller's lower bound on the lengths
   int32_t page_shift;  // log2(page_size) for paged caches
   float scale_log2;    // sm_scale * log2(e)
@@ -242,8 +243,8 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   const int64_t shead_off = static_cast<int64_t>(kvh) * p.cache.scale_stride_h;
   const int page_mask = (1 << p.page_shift) - 1;
   const int tps = p.tokens_per_split;
-  // Clamp so that no access leaves the cache or the launched split range.
-  const int limit = min(p.cache.max_tokens, tps * p.max_splits);
+  // Clamp so that no access leaves the cache (and, paged, no split's range outgrows the LDS block-id cache).
+  const int limit = min(p.cache.max_tokens, p.len_limit);
   // A wave streams chunks of CW consecutive tokens (U loads of RPW rows); its unit of work is a super-chunk of
   // two chunks, one per register buffer. Super-chunk j covers tokens [j * SCW, (j + 1) * SCW).
   constexpr int CW = U * RPW;
@@ -399,7 +400,7 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
     if (p.status && split == 0 && tid == 0) atomicOr(p.status, kStatusLenClamped);
     L = limit;
   }
-  const int n_active = L > 0 ? (L + tps - 1) / tps : 1;
+  const int n_active = L > 0 ? min(p.max_splits, (L + tps - 1) / tps) : 1;
   if (split >= n_active) {
     __syncthreads();  // every wave has read positions[b]
     count_in();

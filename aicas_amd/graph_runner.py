@@ -94,7 +94,9 @@ class AicasGraphDecodeRunner:
     # -- the step --------------------------------------------------------------------------------------
     def _run_step(self) -> None:
         lm = self.language_model
-        hidden = lm.embed_tokens(self.static_input_ids)
+        # token ids bounded on the device: a wrong id gives a wrong token, never a read past the embedding table
+        ids = torch.clamp(self.static_input_ids, 0, lm.embed_tokens.num_embeddings - 1)
+        hidden = lm.embed_tokens(ids)
         position_embeddings = lm.rotary_emb(hidden, self.static_position_ids)
         for layer in lm.layers:
             hidden = layer(hidden, attention_mask=None, position_ids=None, past_key_values=self.cache,
@@ -110,8 +112,11 @@ class AicasGraphDecodeRunner:
         torch.argmax(self.static_logits[:, -1, :], dim=-1, keepdim=True, out=self.static_next_token)
 
     def _set_static(self, on: bool) -> None:
+        # graph mode: every launch is bounded by the capacity and by the lengths at capture, which the replays
+        # only grow (the planner then gives the grid, and the early-fetch kernel variant, of tight bounds)
         for layer in self.cache.layers:
             layer.static_bound = layer.view.max_tokens if on else None
+            layer.static_min = min(layer.host_lens) if on else 0
 
     def maybe_capture(self, past_key_values, prefix_len: int | None, input_ids: torch.Tensor,
                       position_ids: torch.Tensor, cache_position=None, visible_len=None) -> bool:

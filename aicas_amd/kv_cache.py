@@ -73,6 +73,7 @@ class AicasKVCacheLayer(CacheLayerMixin):
         # graph mode: a captured step must stay valid while the lengths grow on the device, so its launches are
         # bounded by this (the capacity) instead of by host_lens, which the capturing runner advances itself
         self.static_bound: int | None = None
+        self.static_min = 0  # graph mode: a lower bound on every length for the rest of the capture's life
 
     # -- CacheLayerMixin -------------------------------------------------------------------------------
     def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
@@ -197,7 +198,8 @@ class AicasKVCacheLayer(CacheLayerMixin):
             # graph mode: nothing host-side may depend on the step (the runner checks capacity and advances
             # host_lens per replay); a token with no slot left is dropped and reported by the kernel
             return ops.decode_attention_append(q, self.view, k_new, v_new, self.seq_lens, sm_scale=sm_scale,
-                                               max_seq_len=self.static_bound, seq_lens_out=self.seq_lens, qk=qk)
+                                               max_seq_len=self.static_bound, min_seq_len=self.static_min,
+                                               seq_lens_out=self.seq_lens, qk=qk)
         if max(self.host_lens) + 1 > self.view.max_tokens:
             raise RuntimeError(f"KV cache capacity exceeded: {max(self.host_lens)} + 1 > {self.view.max_tokens} tokens")
         out = ops.decode_attention_append(

@@ -253,6 +253,11 @@ class BlockPool:
 
 @dataclass(frozen=True)
 class DecodePlan:
+    """A launch plan (``aicas_decode_plan``): a sequence of L tokens is spread over
+    ``min(num_splits, ceil(L / tokens_per_split))`` splits; ``workspace_bytes`` is the workspace the launch needs.
+    Pass the same ``tokens_per_split`` argument (0: automatic) to the launch as to the plan: the library plans
+    the launch itself from the same inputs."""
+
     tokens_per_split: int
     num_splits: int
     workspace_bytes: int
@@ -370,7 +375,7 @@ def decode_attention(
             out4.data_ptr(), out4.stride(0), out4.stride(1),
             _ptr(seq_lens), int(max_seq_len) if seq_lens is None else 0, int(min_seq_len), int(max_seq_len), B,
             Hq, Hkv, D, float(sm_scale),
-            pl.tokens_per_split, workspace.data_ptr(), workspace.numel(), _ptr(status),
+            int(tokens_per_split), workspace.data_ptr(), workspace.numel(), _ptr(status),
             _stream(cache.device),
         )
     )
@@ -459,7 +464,7 @@ def _append_call(q, cache, k_new, v_new, positions, *, sm_scale, max_seq_len, mi
             kn.data_ptr(), kn.stride(0), kn.stride(1), vn.data_ptr(), vn.stride(0), vn.stride(1),
             out4.data_ptr(), out4.stride(0), out4.stride(1),
             positions.data_ptr(), _ptr(seq_lens_out), int(min_seq_len), int(max_seq_len),
-            B, Hq, cache.num_kv_heads, D, float(sm_scale), pl.tokens_per_split)
+            B, Hq, cache.num_kv_heads, D, float(sm_scale), int(tokens_per_split))
     tail = (_ptr(status), _stream(cache.device))
     return out, pl, desc, head, tail
 

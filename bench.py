@@ -27,10 +27,13 @@ all) and steps through them in turn, so that the 256 MB MALL cannot serve the re
 per-layer time. One-step configurations repeat their step with the positions held, so every repeat appends
 at the same position and attends over the same lengths.
 
-Each decode step is captured once as a HIP graph (torch.cuda.CUDAGraph) over per-(step, layer) input and
-output buffers, as a serving loop replays one graph per generated token; the timed region is K back-to-back
-replays bracketed by torch.cuda.synchronize() and HIP events (one event between replays gives the per-step
-median and p90). --mode eager times the same work issued from Python without graphs (host-bound).
+The step is captured once as a HIP graph (torch.cuda.CUDAGraph) and replayed for every generated token, as a
+serving loop (and AicasGraphDecodeRunner) runs it: its launches are bounded by the cache capacity and by the
+prefill length (the lengths only grow from there), read the step-0 input buffers, and bump the lengths on the
+device, so each replay appends one more token and attends over one more. --capture per-step instead captures
+one graph per step with that step's exact bounds and inputs (timed beside it, never the value). The timed region
+is K back-to-back replays bracketed by torch.cuda.synchronize() and HIP events (one event between replays gives
+the per-step median and p90). --mode eager times the same work issued from Python without graphs (host-bound).
 
 Printed JSON line: value = microseconds per decode step (lower is better), plus tokens/s, algorithmic HBM
 bytes per step and GB/s, the decode kernel's roofline (algorithmic bytes per launch / average launch
@@ -64,6 +67,13 @@ def parse_args(argv=None):
     p.add_argument("--steps", type=int, default=0, help="timed steps (0: the configuration's default)")
     p.add_argument("--warmup", type=int, default=16)
     p.add_argument("--mode", choices=("graph", "eager"), default="graph")
+    p.add_argument("--capture", choices=("once", "per-step"), default="once",
+                   help="once: one graph per path, captured with the capacity and the prefill length as the "
+                        "length bounds and replayed for every step while the lengths grow on the device (what "
+                        "a serving loop and AicasGraphDecodeRunner run); per-step: one graph per step with that "
+                        "step's exact bounds")
+    p.add_argument("--compare-capture", type=int, default=1,
+                   help="also time the other capture mode (reported, not the value)")
     p.add_argument("--path", choices=("fused", "separate"), default="fused",
                    help="fused: one launch per layer appends and attends; separate: append kernel + decode kernel")
     p.add_argument("--compare-paths", type=int, default=1, help="also time the other path (reported, not the value)")
@@ -354,8 +364,13 @@ def main(argv=None) -> int:
     ws = ops.Workspace.reserve(dev, plan.workspace_bytes)
     lo, hi = min(base), max(base)
 
-    def step(s, path, kernel_events=None):
-        """One decode step: for every layer append this step's K/V row and attend."""
+    def step(s, path, kernel_events=None, once=False):
+        """One decode step: for every layer append this step's K/V row and attend. once: the launches a serving
+        loop captures a single time and replays for every token — bounded by the capacity and by the prefill
+        length, inputs from the step-0 buffers — instead of this step's own bounds and inputs."""
+        hi_s, lo_s = (cap_seq - 1, lo) if once else (hi + s, lo + s)  # bounds on the lengths before the append
+        if once:
+            s = 0
         for i in range(NL):
             if path == "fused_pool":
                 # the device block pool gives the page the append will write a block (when it has none yet)
@@ -370,9 +385,9 @@ def main(argv=None) -> int:
                     kernel_events[i][0].record()
                 ops.decode_attention_append(
                     q_all[s, i], views[i], kn_all[s, i], vn_all[s, i], shared_lens, sm_scale=SM_SCALE,
-                    max_seq_len=hi + s + 1, min_seq_len=lo + s,
+                    max_seq_len=hi_s + 1, min_seq_len=lo_s,
                     seq_lens_out=shared_lens if (growing and i == NL - 1) else None, out=out_all[s, i],
-                    tokens_per_split=plan.tokens_per_split, workspace=ws, qk=qk,
+                    tokens_per_split=args.tokens_per_split, workspace=ws, qk=qk,
                 )
                 if kernel_events is not None:
                     kernel_events[i][1].record()
@@ -381,8 +396,8 @@ def main(argv=None) -> int:
                 if kernel_events is not None:
                     kernel_events[i][0].record()
                 ops.decode_attention(
-                    q_all[s, i], views[i], sm_scale=SM_SCALE, seq_lens=lens[i], max_seq_len=hi + s + 1,
-                    min_seq_len=lo + s + 1, out=out_all[s, i], tokens_per_split=plan.tokens_per_split, workspace=ws,
+                    q_all[s, i], views[i], sm_scale=SM_SCALE, seq_lens=lens[i], max_seq_len=hi_s + 1,
+                    min_seq_len=lo_s + 1, out=out_all[s, i], tokens_per_split=args.tokens_per_split, workspace=ws,
                 )
                 if kernel_events is not None:
                     kernel_events[i][1].record()
@@ -396,36 +411,37 @@ def main(argv=None) -> int:
 
     stream = torch.cuda.Stream(device=dev)
 
-    def capture(path):
+    def capture(path, once):
+        """once: one graph, replayed for every step (the lengths grow on the device); else one graph per step."""
         graphs = []
         torch.cuda.synchronize()
         with torch.cuda.stream(stream):
-            step(0, path)  # first launch of every kernel outside capture
+            step(0, path, once=once)  # first launch of every kernel outside capture
             torch.cuda.synchronize()
             reset_lens()
             torch.cuda.synchronize()
-            for s in range(n_graph_steps):
+            for s in range(1 if once else n_graph_steps):
                 gr = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(gr, stream=stream):
-                    step(s, path)
+                    step(s, path, once=once)
                 graphs.append(gr)
             torch.cuda.synchronize()
         return graphs
 
-    def run_steps(path, graphs, first, count, events=None):
+    def run_steps(path, graphs, first, count, events=None, once=False):
         for j, s in enumerate(range(first, first + count)):
-            idx = s if growing else 0
+            idx = s if (growing and not once) else 0
             if graphs is not None:
                 graphs[idx].replay()
             else:
-                step(idx, path)
+                step(idx, path, once=once)
             if events is not None:
                 events[j].record()
 
-    def timed(path, graphs):
+    def timed(path, graphs, once):
         with torch.cuda.stream(stream):
             reset_lens()
-            run_steps(path, graphs, 0, W)
+            run_steps(path, graphs, 0, W, once=once)
             torch.cuda.synchronize()
             reset_lens()
             torch.cuda.synchronize()
@@ -433,7 +449,7 @@ def main(argv=None) -> int:
             evs = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
             t0 = time.perf_counter()
             ev0.record()
-            run_steps(path, graphs, 0, K, evs)
+            run_steps(path, graphs, 0, K, evs, once=once)
             torch.cuda.synchronize()
             t1 = time.perf_counter()
         per_step = [ev0.elapsed_time(evs[0]) * 1e3] + [evs[j - 1].elapsed_time(evs[j]) * 1e3 for j in range(1, K)]
@@ -441,27 +457,33 @@ def main(argv=None) -> int:
 
     path = args.path
     other = "separate" if path == "fused" else "fused"
-    graphs = capture(path) if args.mode == "graph" else None
-    gpu_ms, wall_ms, per_step_us = timed(path, graphs)
+    once = args.capture == "once"
+    graphs = capture(path, once) if args.mode == "graph" else None
+    gpu_ms, wall_ms, per_step_us = timed(path, graphs, once)
     us_graph_step = gpu_ms * 1e3 / K  # one replay: NL layer-steps
     us_per_step = us_graph_step * layer_weight
+    other_capture_us = None
+    if args.compare_capture and args.mode == "graph":
+        graphs_c = capture(path, not once)
+        other_capture_us = timed(path, graphs_c, not once)[0] * 1e3 / K * layer_weight
+        del graphs_c
     other_us = None
     if args.compare_paths:
-        graphs_other = capture(other) if args.mode == "graph" else None
-        other_us = timed(other, graphs_other)[0] * 1e3 / K * layer_weight
+        graphs_other = capture(other, once) if args.mode == "graph" else None
+        other_us = timed(other, graphs_other, once)[0] * 1e3 / K * layer_weight
         del graphs_other
     pool_us = None
     if w.paged and args.compare_pool:
         # one pool per cache instance, every block free; the tables were filled at set-up, so a step's
         # allocation scans its pages and pops nothing (a page is new only every page_size steps)
         pools = [ops.BlockPool(views[i].k.shape[0], dev) for i in range(NL)]
-        graphs_pool = capture("fused_pool") if args.mode == "graph" else None
-        pool_us = timed("fused_pool", graphs_pool)[0] * 1e3 / K * layer_weight
+        graphs_pool = capture("fused_pool", once) if args.mode == "graph" else None
+        pool_us = timed("fused_pool", graphs_pool, once)[0] * 1e3 / K * layer_weight
         del graphs_pool
     qk_us = None
     if args.compare_qk:
-        graphs_qk = capture("fused_qk") if args.mode == "graph" else None
-        qk_us = timed("fused_qk", graphs_qk)[0] * 1e3 / K * layer_weight
+        graphs_qk = capture("fused_qk", once) if args.mode == "graph" else None
+        qk_us = timed("fused_qk", graphs_qk, once)[0] * 1e3 / K * layer_weight
         del graphs_qk
 
     lens_per_step = [[L + (s if growing else 0) + 1 for L in base] for s in range(K)]
@@ -483,7 +505,7 @@ def main(argv=None) -> int:
                    for _ in range(kt_steps)]
             torch.cuda._sleep(int(1.0e8))
             for s in range(kt_steps):
-                step(s if growing else 0, path, kernel_events=evs[s])
+                step(s if growing else 0, path, kernel_events=evs[s], once=once)
             torch.cuda.synchronize()
             for s in range(kt_steps):
                 for i in range(NL):
@@ -534,16 +556,17 @@ def main(argv=None) -> int:
         with torch.cuda.stream(stream):
             reset_lens()
             torch.cuda.synchronize()
-            run_steps(path, graphs, 0, check_steps)
+            run_steps(path, graphs, 0, check_steps, once=once)
             torch.cuda.synchronize()
+        src = (lambda s_: 0) if once else (lambda s_: s_)  # step -> the input buffers its launches read
         seqs = list(range(B)) if B <= 8 else list(range(0, B, B // 8))[:8]
         for i in sorted({0, NL // 2, NL - 1}):
             for b in seqs:
                 s = check_steps - 1
                 L = base[b] + s + 1
                 k, v = cached(i, b, L)
-                expect = ref.decode_fp64(q_all[s, i, b : b + 1].cpu(), k[None], v[None], SM_SCALE, G)
-                err = (out_all[s, i, b : b + 1].double().cpu() - expect).abs().max().item()
+                expect = ref.decode_fp64(q_all[src(s), i, b : b + 1].cpu(), k[None], v[None], SM_SCALE, G)
+                err = (out_all[src(s), i, b : b + 1].double().cpu() - expect).abs().max().item()
                 max_err = max(max_err, err)
         if not w.paged:
             # the appended rows are bit-identical to the torch.cat cache
@@ -551,7 +574,7 @@ def main(argv=None) -> int:
                 for s in range(check_steps):
                     for b in seqs:
                         assert torch.equal(views[i].k[b, :, base[b] + s].cpu().view(torch.int16),
-                                           kn_all[s, i, b, :, 0].cpu().view(torch.int16))
+                                           kn_all[src(s), i, b, :, 0].cpu().view(torch.int16))
 
     # ---- CPU baseline: the oracle (reference PyTorch path) on the host cores, same inputs, first steps (a
     # one-step configuration repeats its step from the same cache)
@@ -653,8 +676,8 @@ def main(argv=None) -> int:
             "name": args.config, "batch": B, "layers": w.layers, "cache_instances": NL,
             "cached_before": base[0] if w.len_range is None else [lo, hi],
             "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "paged": w.paged, "page_size": page,
-            "mode": args.mode, "path": path, "tokens_per_split": plan.tokens_per_split,
-            "num_splits": plan.num_splits,
+            "mode": args.mode, "capture": args.capture, "path": path,
+            "tokens_per_split": plan.tokens_per_split, "num_splits": plan.num_splits,
         },
         "us_per_step_median": round(percentile(per_step_us, 0.5) * layer_weight, 2),
         "us_per_step_p90": round(percentile(per_step_us, 0.9) * layer_weight, 2),
@@ -664,6 +687,8 @@ def main(argv=None) -> int:
         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
         "wall_ms": round(wall_ms, 3),
         f"{other}_path_us_per_step": None if other_us is None else round(other_us, 2),
+        ("per_step_capture_us_per_step" if once else "single_capture_us_per_step"):
+            None if other_capture_us is None else round(other_capture_us, 2),
         "fused_qk_path_us_per_step": None if qk_us is None else round(qk_us, 2),
         "fused_with_block_pool_us_per_step": None if pool_us is None else round(pool_us, 2),
         "roofline": {

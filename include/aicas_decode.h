@@ -103,8 +103,11 @@ int aicas_kv_append(const aicas_kv_cache_t* cache, int32_t src_dtype, const void
                     hipStream_t stream);
 
 /*
- * Launch plan for aicas_decode_attention: the token range per split (tokens_per_split_hint, or 0 to choose
- * automatically), the number of splits covering max_seq_len, and the workspace size in bytes. The
+ * Launch plan for aicas_decode_attention: the split size (tokens_per_split_hint, or 0 to choose automatically)
+ * and split count — a sequence of L tokens is spread over min(num_splits, ceil(L / tokens_per_split)) splits —
+ * and the workspace size in bytes. With few (batch row, kv head) pairs the automatic plan keeps its split count
+ * whatever max_seq_len is, once sequences are long enough, so a launch sized for a loose bound (a graph captured
+ * at the cache capacity) runs the grid a tight bound gives. A launch plans itself from the same arguments. The
  * workspace starts with 512 KiB of counters at fixed offsets, followed by the split partials; it must be
  * zero-filled once when first allocated, and the kernels leave the counters at zero after every launch, so
  * launches of any shapes may share one workspace in turn. Two launches that may run concurrently need two
@@ -119,8 +122,10 @@ int aicas_decode_plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int3
  * out[b, hq, :] = softmax(q[b, hq, :] . K[b, hq / G, t, :] * sm_scale over t < L_b) . V[b, hq / G, t, :],
  * G = num_q_heads / num_kv_heads, L_b = seq_lens[b] (or uniform_len when seq_lens is NULL).
  * q and out are [B, Hq, D] with element strides (head_dim stride 1) in q_dtype (bf16 or fp16); a 16-bit
- * cache must have kv_dtype == q_dtype. max_seq_len must bound every L_b: longer sequences are clamped and
- * AICAS_STATUS_LEN_CLAMPED is set. An empty sequence (L_b == 0) yields zeros. head_dim in {16, 32, 64, 128},
+ * cache must have kv_dtype == q_dtype. max_seq_len sizes the launch (plan and workspace); a longer L_b is still
+ * attended in full while the cache holds it (paged caches: up to the plan's per-split block-table limit, at least
+ * max_seq_len), and clamped beyond that, with AICAS_STATUS_LEN_CLAMPED set. An empty sequence (L_b == 0) yields
+ * zeros. head_dim in {16, 32, 64, 128},
  * G in {1, 2, 4, 8}. tokens_per_split as from aicas_decode_plan (0 = automatic). min_len is a lower bound on every
  * L_b that the caller may pass (0 if unknown): when it keeps every split of a contiguous cache busy, the launch
  * fetches its first rows before reading the lengths. Results never depend on it; a wrong bound costs bandwidth.

@@ -79,10 +79,13 @@ def _plan(kv_dtype, B, Hq, Hkv, D, L, page=0, hint=0):
 
 @pytest.mark.parametrize("B, Hkv, L", [(8, 8, 2113), (1, 8, 32832), (64, 8, 4097), (32, 8, 8193), (1, 2, 1)])
 def test_plan_covers_every_token(B, Hkv, L):
+    """A sequence of L tokens takes min(num_splits, ceil(L / tokens_per_split)) splits: at least one, never more
+    than planned; the split size is a whole number of workgroup loads; the workspace holds every split's
+    partial."""
     for kv in (_lib.DTYPE_BF16, _lib.DTYPE_FP8_E4M3):
         rc, tps, ns, wb = _plan(kv, B, 2 * Hkv, Hkv, 128, L)
         assert rc == _lib.OK
-        assert tps * ns >= L and tps * (ns - 1) < L
+        assert ns >= 1 and 1 <= min(ns, -(-L // tps)) <= ns
         rows = 16 if kv == _lib.DTYPE_BF16 else 32  # tokens one workgroup load covers at D=128
         assert tps % rows == 0
         parts = B * 2 * Hkv * ns
@@ -99,6 +102,11 @@ def test_plan_split_counts():
     assert _plan(bf, 1, 16, 8, 128, 1025)[1:3] == (128, 9)  # B=1 L=1024: 128 tokens = 4 waves x 32
     assert _plan(f8, 32, 16, 8, 128, 8193, 16)[2] == 2  # 256 pairs: 7/4 per CU
     assert _plan(bf, 64, 16, 8, 128, 4097)[2] == 1     # 512 pairs
+    # few pairs: the split size is the minimum (two chunks per wave) and the count does not follow a loose bound
+    assert _plan(bf, 8, 16, 8, 128, 2049)[1:3] == _plan(bf, 8, 16, 8, 128, 65536)[1:3] == (128, 4)
+    assert _plan(bf, 1, 16, 8, 128, 32769)[1:3] == _plan(bf, 1, 16, 8, 128, 1 << 20)[1:3] == (128, 28)
+    # many pairs: in proportion to the bound, so that the longest sequences split
+    assert _plan(bf, 64, 16, 8, 128, 8192)[2] == 1 and _plan(f8, 32, 16, 8, 128, 4096, 16)[2] == 2
     for B in range(1, 25):
         for L in (300, 2049, 9000):
             rc, tps, ns, _ = _plan(bf, B, 16, 8, 128, L)

@@ -318,3 +318,30 @@ def test_min_seq_len_hint_gives_identical_results(dev, tps):
                                      min_seq_len=min(lens), seq_lens_out=pos_b, tokens_per_split=tps)
     assert torch.equal(fa.cpu(), fb.cpu())
     assert torch.equal(view.k.cpu().view(torch.int16), view_b.k.cpu().view(torch.int16))
+
+
+@pytest.mark.parametrize("B, lens, cap", [(8, [2048] * 8, 4096), (1, [32768], 65536), (2, [700, 1300], 8192)])
+def test_loose_bound_runs_the_tight_grid(dev, B, lens, cap):
+    """With few (batch row, kv head) pairs each sequence takes its split count from its own length, so a launch
+    bounded by the cache capacity (a graph captured once for every later step) gives the bits of a launch bounded
+    by the exact length: the same splits, merged in the same order."""
+    gen = torch.Generator().manual_seed(91)
+    Hkv, G, D = 8, 2, 128
+    q = _rand((B, Hkv * G, 1, D), gen).to(dev)
+    view = ops.KVCacheView(_rand((B, Hkv, cap, D), gen).to(dev), _rand((B, Hkv, cap, D), gen).to(dev))
+    kn = _rand((B, Hkv, 1, D), gen).to(dev)
+    sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    tight = ops.decode_attention(q, view, sm_scale=D ** -0.5, seq_lens=sl, max_seq_len=max(lens))
+    loose = ops.decode_attention(q, view, sm_scale=D ** -0.5, seq_lens=sl, max_seq_len=cap)
+    assert torch.equal(tight.cpu().view(torch.int16), loose.cpu().view(torch.int16))
+    outs = []
+    for bound, lo in ((max(lens) + 1, min(lens)), (cap, min(lens)), (cap, 0)):
+        vw, pos = ops.KVCacheView(view.k.clone(), view.v.clone()), sl.clone()
+        outs.append(ops.decode_attention_append(q, vw, kn, kn, pos, sm_scale=D ** -0.5, max_seq_len=bound,
+                                                min_seq_len=lo, seq_lens_out=pos).cpu())
+        assert pos.cpu().tolist() == [L + 1 for L in lens]
+    assert all(torch.equal(o.view(torch.int16), outs[0].view(torch.int16)) for o in outs[1:])
+    kd, vd = view.k.cpu().float(), view.v.cpu().float()
+    expect = ref.ragged_decode(q.cpu().float(), [kd[b, :, :lens[b]] for b in range(B)],
+                               [vd[b, :, :lens[b]] for b in range(B)], D ** -0.5, G).float()
+    torch.testing.assert_close(loose.float().cpu(), expect, atol=2e-2, rtol=1e-2)
