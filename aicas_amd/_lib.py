@@ -34,6 +34,7 @@ STATUS_LEN_CLAMPED = 1
 STATUS_BLOCK_OUT_OF_RANGE = 2
 STATUS_APPEND_OVERFLOW = 4
 STATUS_OUT_OF_BLOCKS = 8
+STATUS_NONFINITE_ROW = 16
 
 # Entry points declared in include/aicas_decode.h, in declaration order.
 EXPORTED_SYMBOLS = (

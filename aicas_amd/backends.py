@@ -111,11 +111,18 @@ def text_triton_attention(
         )
 
     meta = kv_descriptor(key)
-    # A ragged, paged or fp8 cache defines visibility through its own per-sequence lengths; HF's padding
-    # mask cannot describe it, so such caches always take the decode kernel for q_len == 1.
-    mask_ok = attention_mask is None or (meta is not None and not meta.dense)
+    # A ragged, paged or fp8 aicas cache defines visibility through its own per-sequence lengths and can only be
+    # read by the decode kernel, which has no per-token mask. HF hands an attention function a mask only when
+    # some position is padding (flash_attention_mask returns None for an all-ones mask), so a mask here means
+    # the kernel would attend to pad tokens: refused rather than silently ignored. Dense caches take the SDPA
+    # route with the mask, as the reference does (backends.py:235-260).
+    if attention_mask is not None and meta is not None and not meta.dense:
+        raise ValueError(
+            "a padding mask reached the decode path of a paged, fp8 or ragged aicas cache, which attends to every "
+            "cached token of a sequence: use a dense 16-bit AicasDecodeCache (or DynamicCache) for padded batches"
+        )
     can_use_decode = (
-        mask_ok
+        attention_mask is None
         and query.shape[2] == 1
         and dropout == 0.0
         and can_use_gqa_decode_attention(query, key, value, num_key_value_groups=num_key_value_groups)

@@ -16,6 +16,7 @@ enum StatusBits : int32_t {
   kStatusBlockOutOfRange = 2, // a block-table entry was outside [0, num_blocks)
   kStatusAppendOverflow = 4,  // an append position was outside the cache; the row was dropped
   kStatusOutOfBlocks = 8,     // the block pool ran out: a page was left without a block
+  kStatusNonFiniteRow = 16,   // an fp8 cache received a row holding NaN or +-Inf (stored poisoned)
 };
 
 constexpr int kWave = 64;
@@ -152,6 +153,24 @@ __device__ __forceinline__ float group_max(float x) {
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Scale of one fp8 cache row spread over N aligned lanes (VEC values each; every lane of the row takes part):
+// amax / 448, 0 for an all-zero row. A row holding any NaN or +-Inf gets a NaN scale (and, from the caller's
+// `scale > 0` test, all-zero codes), so that it dequantises to NaN everywhere, as the unquantised row would make
+// every score that touches it non-finite; `nonfinite` reports it.
+template <int N, int VEC>
+__device__ __forceinline__ float fp8_row_scale(const float* f, bool& nonfinite) {
+  float amax = 0.0f, bad = 0.0f;
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    const float a = fabsf(f[i]);
+    amax = fmaxf(amax, a);
+    bad = a <= 3.402823466e38f ? bad : 1.0f;  // false for NaN and Inf
+  }
+  amax = group_max<N>(amax);
+  nonfinite = group_max<N>(bad) > 0.0f;
+  return nonfinite ? __builtin_nanf("") : amax / 448.0f;
+}
 
 // A 16-byte load of data read once per launch (cache rows): non-temporal (global_load_dwordx4 ... nt), so the
 // stream does not allocate in the caches on its way through. The decode kernel's access pattern as a pure read

@@ -42,10 +42,12 @@
 // cache: every workgroup stages the rows in LDS and the wave that streams the token selects them in before
 // consuming its chunk, and split 0 writes the row into the cache (quantized on write for fp8 caches, with the
 // attention then using the dequantised row, exactly what a separate append followed by attention would read).
-// Every workgroup of batch row b counts itself in once all its waves have read positions[b]; the last one to do
-// so stores positions[b] + 1 to seq_lens_out[b] (which may alias positions) as it exits, so no workgroup can
-// read a bumped length.
+// Every workgroup of batch row b counts itself in on its way out, once all its waves have read positions[b];
+// the last one to do so stores positions[b] + 1 to seq_lens_out[b] (which may alias positions), so no workgroup
+// can read a bumped length.
 #pragma once
+
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -670,11 +672,9 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
                                  new_raw[1].x, new_raw[1].y, new_raw[1].z, new_raw[1].w};
 #pragma unroll
           for (int i = 0; i < 8; ++i) unpack2<Q_DT>(w[i], f[2 * i], f[2 * i + 1]);
-          float amax = 0.0f;
-#pragma unroll
-          for (int i = 0; i < VEC; ++i) amax = fmaxf(amax, fabsf(f[i]));
-          amax = group_max<R>(amax);
-          const float scale = amax / 448.0f;
+          bool nonfinite;
+          const float scale = fp8_row_scale<R, VEC>(f, nonfinite);
+          if (nonfinite && ok && c == 0 && p.status) atomicOr(p.status, kStatusNonFiniteRow);
           uint32_t packed[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
           for (int i = 0; i < VEC; ++i) {
@@ -832,7 +832,8 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
       const int idx = tid + c * kBlockThreads;
       if (idx < G * D) {
         const int hq = kvh * G + idx / D;
-        outb[hq * p.out_stride_h + idx % D] = from_f32<Q_DT>(ls[c] > 0.0f ? a[c] / ls[c] : 0.0f);
+        // an empty sequence (l exactly 0) gives zeros; a NaN l (a poisoned fp8 row) stays NaN
+        outb[hq * p.out_stride_h + idx % D] = from_f32<Q_DT>(ls[c] == 0.0f ? 0.0f : a[c] / ls[c]);
       }
     }
     // QK: the prepared q goes out from the workgroup that writes the output, after every split of the pair has
@@ -883,41 +884,64 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
     return;
   }
 
-  // One online pass over the splits in order, MB at a time: the MB partials' loads are issued unconditionally
-  // (past the last split they repeat it, masked below), so they are in flight together and the merge costs
-  // about n_active / MB memory round trips; loads behind per-split branches would each end in a wait of their
-  // own.
-  constexpr int MB = 8;
+  // One online pass over the splits in order, a batch of MB splits at a time for all of this thread's cells: the
+  // batch's loads are issued unconditionally (past the last split they repeat it, masked below), so they are in
+  // flight together and the merge costs ceil(n_active / MB) memory round trips; loads behind per-split branches
+  // would each end in a wait of their own. A batch keeps at most 48 loads in flight per thread: 16 splits for one
+  // cell (8 when at most 8 splits exist, so that few repeats go out), 8 for two cells, 4 for four.
   float rl[CPT], ra[CPT];
+  auto merge_all = [&](auto mb_tag) {
+    constexpr int MB = decltype(mb_tag)::value;
+    float M[CPT], ls[CPT], a[CPT];
+    int64_t hbase[CPT];
+    int dcol[CPT];
 #pragma unroll
-  for (int c = 0; c < CPT; ++c) {
-    const int idx = min(tid + c * kBlockThreads, G * D - 1);
-    const int64_t hbase = pair_base + (idx / D) * p.max_splits;
-    const int d = idx % D;
-    float M = kNegBig, ls = 0.0f, a = 0.0f;
+    for (int c = 0; c < CPT; ++c) {
+      const int idx = min(tid + c * kBlockThreads, G * D - 1);
+      hbase[c] = pair_base + (idx / D) * p.max_splits;
+      dcol[c] = idx % D;
+      M[c] = kNegBig;
+      ls[c] = 0.0f;
+      a[c] = 0.0f;
+    }
     for (int i0 = 0; i0 < n_active; i0 += MB) {
-      float mi[MB], li[MB], ai[MB];
+      float mi[CPT][MB], li[CPT][MB], ai[CPT][MB];
 #pragma unroll
-      for (int j = 0; j < MB; ++j) {
-        const int i = min(i0 + j, n_active - 1);
-        mi[j] = load_agent(p.ws_ml + 2 * (hbase + i));
-        li[j] = load_agent(p.ws_ml + 2 * (hbase + i) + 1);
-        ai[j] = load_agent(p.ws_acc + (hbase + i) * D + d);
+      for (int c = 0; c < CPT; ++c) {
+#pragma unroll
+        for (int j = 0; j < MB; ++j) {
+          const int i = min(i0 + j, n_active - 1);
+          mi[c][j] = load_agent(p.ws_ml + 2 * (hbase[c] + i));
+          li[c][j] = load_agent(p.ws_ml + 2 * (hbase[c] + i) + 1);
+          ai[c][j] = load_agent(p.ws_acc + (hbase[c] + i) * D + dcol[c]);
+        }
       }
 #pragma unroll
-      for (int j = 0; j < MB; ++j) {
-        if (i0 + j < n_active) {
-          const float mn = fmaxf(M, mi[j]);
-          const float c_old = fast_exp2(M - mn);
-          const float c_new = fast_exp2(mi[j] - mn);
-          ls = ls * c_old + li[j] * c_new;
-          a = a * c_old + ai[j] * c_new;
-          M = mn;
+      for (int c = 0; c < CPT; ++c) {
+#pragma unroll
+        for (int j = 0; j < MB; ++j) {
+          if (i0 + j < n_active) {
+            const float mn = fmaxf(M[c], mi[c][j]);
+            const float c_old = fast_exp2(M[c] - mn);
+            const float c_new = fast_exp2(mi[c][j] - mn);
+            ls[c] = ls[c] * c_old + li[c][j] * c_new;
+            a[c] = a[c] * c_old + ai[c][j] * c_new;
+            M[c] = mn;
+          }
         }
       }
     }
-    rl[c] = ls;
-    ra[c] = a;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      rl[c] = ls[c];
+      ra[c] = a[c];
+    }
+  };
+  if constexpr (CPT == 1) {
+    if (n_active > 8) merge_all(std::integral_constant<int, 16>{});
+    else merge_all(std::integral_constant<int, 8>{});
+  } else {
+    merge_all(std::integral_constant<int, (CPT >= 4 ? 4 : 8)>{});
   }
   write_out(rl, ra);
   if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -116,11 +116,9 @@ __global__ __launch_bounds__(kBlockThreads) void kv_append_kernel(AppendParams p
       unpack2<SRC_DT>(x[k].y, f[2], f[3]);
       unpack2<SRC_DT>(x[k].z, f[4], f[5]);
       unpack2<SRC_DT>(x[k].w, f[6], f[7]);
-      float amax = 0.0f;
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) amax = fmaxf(amax, fabsf(f[i]));
-      amax = group_max<R>(amax);  // every lane of the row takes part, so the DPP exchange is complete
-      const float scale = amax / 448.0f;
+      bool nonfinite;
+      const float scale = fp8_row_scale<R, VEC>(f, nonfinite);  // every lane of the row takes part
+      if (nonfinite && ok && lane == 0 && p.status) atomicOr(p.status, kStatusNonFiniteRow);
       uint32_t packed[2] = {0u, 0u};
 #pragma unroll
       for (int i = 0; i < VEC; ++i) {

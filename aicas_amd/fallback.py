@@ -31,6 +31,19 @@ def _load_sdpa_attention_forward():
     return sdpa_attention_forward
 
 
+def _padding_mask_4d(attention_mask: torch.Tensor, q_len: int, kv_len: int, causal: bool) -> torch.Tensor:
+    """The 2-D padding mask ``[B, kv]`` an attention function receives when its mask interface is
+    flash_attention_2's (transformers/masking_utils.py:607-647, what install_qwen3vl_triton_attention aliases) ->
+    the 4-D boolean ``[B, 1, q, kv]`` mask HF's own SDPA path builds for the same step
+    (masking_utils.sdpa_mask, queries at the last q_len positions). SDPA cannot broadcast a 2-D ``[B, kv]`` mask
+    over ``[B, H, q, kv]`` scores for B > 1, which is what the reference's fallback would hand it."""
+    from transformers.masking_utils import bidirectional_mask_function, causal_mask_function, sdpa_mask
+
+    return sdpa_mask(batch_size=attention_mask.shape[0], q_length=q_len, kv_length=kv_len, q_offset=kv_len - q_len,
+                     kv_offset=0, mask_function=causal_mask_function if causal else bidirectional_mask_function,
+                     attention_mask=attention_mask.bool(), allow_is_causal_skip=False, device=attention_mask.device)
+
+
 def sdpa_fallback(
     module: torch.nn.Module,
     query: torch.Tensor,
@@ -48,6 +61,9 @@ def sdpa_fallback(
             "SDPA cannot consume it (decode with attention_mask=None, q_len=1)"
         )
     sdpa_attention_forward = _load_sdpa_attention_forward()
+    if sdpa_attention_forward is not None and attention_mask is not None and attention_mask.dim() == 2:
+        causal = is_causal if is_causal is not None else getattr(module, "is_causal", True)
+        attention_mask = _padding_mask_4d(attention_mask, query.shape[2], key.shape[2], bool(causal))
     if sdpa_attention_forward is not None:
         return sdpa_attention_forward(
             module, query, key, value, attention_mask, dropout=dropout, scaling=scaling, is_causal=is_causal,

@@ -162,6 +162,22 @@ class AicasKVCacheLayer(CacheLayerMixin):
     def offload(self):
         raise NotImplementedError("AicasKVCacheLayer keeps its storage on the GPU")
 
+    # Beam search and cache surgery reorder or cut HF's per-layer keys/values tensors; here the kernels read the
+    # storage through a descriptor (device lengths, block table, scales) that those edits would leave behind, so
+    # they are refused rather than half-applied. The reference turns its custom caches off for num_beams != 1
+    # (dujunbaoV1/evaluation_wrapper.py:1670, :2592).
+    def reorder_cache(self, beam_idx: torch.LongTensor) -> None:
+        raise NotImplementedError("AicasKVCacheLayer does not support beam search (reorder_cache); use num_beams=1")
+
+    def crop(self, max_length: int) -> None:
+        raise NotImplementedError("AicasKVCacheLayer does not support crop")
+
+    def batch_repeat_interleave(self, repeats: int) -> None:
+        raise NotImplementedError("AicasKVCacheLayer does not support batch_repeat_interleave")
+
+    def batch_select_indices(self, indices: torch.Tensor) -> None:
+        raise NotImplementedError("AicasKVCacheLayer does not support batch_select_indices")
+
     def prefetch(self):
         return None
 

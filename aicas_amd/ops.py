@@ -89,6 +89,10 @@ class KVCacheView:
             bt = self.block_table
             if bt.dtype != torch.int32 or bt.dim() != 2 or bt.stride(1) != 1:
                 raise AicasError(_lib.ERR_INVALID, "block_table must be int32 [B, max_blocks] with unit column stride")
+            if bt.shape[1] != bt.stride(0):
+                # the kernels take a row's width to be its stride (aicas_kv_cache_t has no width field): a
+                # column-sliced table would let a length past the width read the next row's entries
+                raise AicasError(_lib.ERR_INVALID, "block_table rows must be contiguous (width == row stride)")
 
     @property
     def is_fp8(self) -> bool:
@@ -140,8 +144,6 @@ class KVCacheView:
             d.block_table = self.block_table.data_ptr()
             d.block_table_stride = self.block_table.stride(0)
             d.num_blocks = self.k.shape[0]
-            if self.block_table.shape[1] > self.block_table.stride(0):
-                raise AicasError(_lib.ERR_INVALID, "block_table rows overlap")
         else:
             d.num_blocks = self.k.shape[0]
         return d

@@ -54,6 +54,7 @@ extern "C" {
 #define AICAS_STATUS_BLOCK_OUT_OF_RANGE 2
 #define AICAS_STATUS_APPEND_OVERFLOW 4
 #define AICAS_STATUS_OUT_OF_BLOCKS 8
+#define AICAS_STATUS_NONFINITE_ROW 16 /* an fp8 cache received a row holding NaN or +-Inf: stored poisoned */
 
 /*
  * A KV cache. Two layouts share one description:
@@ -88,8 +89,9 @@ typedef struct aicas_kv_cache {
  * head_dim stride 1, strides in elements) go to token position positions[b] + j of sequence b. A 16-bit
  * cache must have kv_dtype == src_dtype and receives the rows bit for bit; an fp8 cache receives
  * e4m3(clamp(x / s, -448, 448)) with s = max|row| / 448 stored in k_scale / v_scale (s = 0 and all-zero
- * codes for an all-zero row). If seq_lens_out is not NULL, seq_lens_out[b] = positions[b] + n_new is
- * written after the rows; it may alias positions. A row whose position falls outside the cache is dropped
+ * codes for an all-zero row; a row holding any NaN or +-Inf is stored poisoned, s = NaN and all-zero codes, so
+ * that it dequantises to NaN, and AICAS_STATUS_NONFINITE_ROW is set). If seq_lens_out is not NULL,
+ * seq_lens_out[b] = positions[b] + n_new is written after the rows; it may alias positions. A row whose position falls outside the cache is dropped
  * and AICAS_STATUS_APPEND_OVERFLOW is ORed into *status (status may be NULL). batch <= 65535. A decode step's
  * append is one launch; a prefill-sized one (a prompt written into the cache) spreads each sequence's rows
  * over many workgroups and bumps the lengths in a second, one-thread-per-sequence launch.

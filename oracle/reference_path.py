@@ -187,14 +187,19 @@ def e4m3_decode_table() -> torch.Tensor:
 def fp8_quantize_rows(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Quantize-on-write for fp8 caches: rows along the last axis; scale = amax/448 (fp32) per row;
     codes = e4m3(clamp(x / scale, -448, 448)) (torch's cast rounds to nearest even; without the clamp it
-    would turn values above 448 into NaN); an all-zero row has scale 0 and zero codes.
+    would turn values above 448 into NaN); an all-zero row has scale 0 and zero codes. A row holding any NaN
+    or +-Inf is stored poisoned: scale NaN and zero codes, so that it dequantises to NaN everywhere (the
+    unquantised row would make every score that touches it non-finite). The fp8 layout replaces the
+    reference's KIVI codec (new KV cache/evaluation_wrapper.py:68-140), which defines no such case.
     Returns (codes as torch.float8_e4m3fn, scales float32 of shape x.shape[:-1])."""
     xf = x.float()
-    amax = xf.abs().amax(dim=-1)
-    scale = amax / FP8_MAX
-    safe = torch.where(scale > 0, scale, torch.ones_like(scale))
-    y = (xf / safe[..., None]).clamp(-FP8_MAX, FP8_MAX)
-    y = torch.where(scale[..., None] > 0, y, torch.zeros_like(y))
+    finite = torch.isfinite(xf).all(dim=-1)
+    amax = torch.where(finite[..., None], xf, torch.zeros_like(xf)).abs().amax(dim=-1)
+    scale = torch.where(finite, amax / FP8_MAX, torch.full_like(amax, float("nan")))
+    ok = finite & (scale > 0)
+    safe = torch.where(ok, scale, torch.ones_like(scale))
+    y = (torch.where(ok[..., None], xf, torch.zeros_like(xf)) / safe[..., None]).clamp(-FP8_MAX, FP8_MAX)
+    y = torch.where(ok[..., None], y, torch.zeros_like(y))
     return y.to(torch.float8_e4m3fn), scale
 
 

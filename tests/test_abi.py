@@ -44,7 +44,8 @@ def test_constants_match_header():
                         ("AICAS_ERR_LAUNCH", _lib.ERR_LAUNCH), ("AICAS_STATUS_LEN_CLAMPED", _lib.STATUS_LEN_CLAMPED),
                         ("AICAS_STATUS_BLOCK_OUT_OF_RANGE", _lib.STATUS_BLOCK_OUT_OF_RANGE),
                         ("AICAS_STATUS_APPEND_OVERFLOW", _lib.STATUS_APPEND_OVERFLOW),
-                        ("AICAS_STATUS_OUT_OF_BLOCKS", _lib.STATUS_OUT_OF_BLOCKS)]:
+                        ("AICAS_STATUS_OUT_OF_BLOCKS", _lib.STATUS_OUT_OF_BLOCKS),
+                        ("AICAS_STATUS_NONFINITE_ROW", _lib.STATUS_NONFINITE_ROW)]:
         assert re.search(rf"#define {name} {value}\b", text), name
 
 

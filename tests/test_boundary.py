@@ -231,3 +231,100 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     with pytest.raises(_lib.AicasError, match="not built"):
         _lib.lib()
     assert patch.hip_decode_available() is False
+
+
+def test_padding_mask_on_kernel_only_cache_is_refused(monkeypatch):
+    """A padding mask cannot be applied to a paged / fp8 / ragged aicas cache (the kernel attends to every cached
+    token of a sequence): the attention function raises instead of dropping the mask. A dense cache with a mask
+    takes the SDPA route, as the reference's does."""
+    from aicas_amd.gqa_decode_attention import AicasKV
+
+    monkeypatch.setattr(backends, "can_use_gqa_decode_attention", lambda *args, **kwargs: True)
+    monkeypatch.setattr(backends, "gqa_decode_attention",
+                        lambda *a, **k: (_ for _ in ()).throw(AssertionError("kernel must not run with a mask")))
+    module = DummyAttentionModule(num_key_value_groups=2)
+    q, k, v = torch.randn(2, 4, 1, 8), torch.randn(2, 2, 6, 8), torch.randn(2, 2, 6, 8)
+    mask = torch.tensor([[0, 1, 1, 1, 1, 1], [1, 1, 1, 1, 1, 1]], dtype=torch.bool)
+    k._aicas_kv = AicasKV(cache=None, seq_lens=None, max_seq_len=6, batch=2, dense=False)
+    with pytest.raises(ValueError, match="padding mask"):
+        text_triton_attention(module, q, k, v, attention_mask=mask)
+    recorded = {}
+
+    def fake_sdpa(*args, **kwargs):
+        recorded["mask"] = args[4] if len(args) > 4 else kwargs.get("attention_mask")
+        return torch.zeros(2, 1, 4, 8), None
+
+    monkeypatch.setattr(backends, "sdpa_fallback", fake_sdpa)
+    k._aicas_kv = AicasKV(cache=None, seq_lens=None, max_seq_len=6, batch=2, dense=True)
+    text_triton_attention(module, q, k, v, attention_mask=mask)
+    assert recorded["mask"] is mask
+
+
+def test_cache_layer_refuses_beam_reordering():
+    """Beam search would reorder HF's keys/values and leave the kernels' descriptor behind: refused."""
+    from aicas_amd.kv_cache import AicasKVCacheLayer
+
+    layer = AicasKVCacheLayer(max_cache_len=16)
+    for call in (lambda: layer.reorder_cache(torch.tensor([1, 0])), lambda: layer.crop(4),
+                 lambda: layer.batch_repeat_interleave(2), lambda: layer.batch_select_indices(torch.tensor([0]))):
+        with pytest.raises(NotImplementedError):
+            call()
+
+
+def test_column_sliced_block_table_is_refused():
+    """The kernels take a block-table row's width to be its stride: a column-sliced table is refused."""
+    from aicas_amd import ops
+
+    pool = torch.zeros((8, 2, 16, 64), dtype=torch.bfloat16)
+    table = torch.arange(8, dtype=torch.int32).view(2, 4)
+    ops.KVCacheView(pool, pool.clone(), block_table=table)
+    ops.KVCacheView(pool, pool.clone(), block_table=table[1:2])
+    with pytest.raises(_lib.AicasError, match="contiguous"):
+        ops.KVCacheView(pool, pool.clone(), block_table=table[:, :2])
+
+
+def test_left_padded_batch_matches_hf_sdpa_on_cpu():
+    """A left-padded batch through the installed backend (whose mask interface hands attention functions HF's 2-D
+    padding mask) gives HF's own SDPA path's hidden states, prefill and decode, on the CPU route."""
+    from transformers.cache_utils import DynamicCache
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLTextConfig
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import Qwen3VLTextModel
+
+    from aicas_amd import patch
+    from aicas_amd.backends import TEXT_BACKEND_KEY
+
+    cfg = Qwen3VLTextConfig(vocab_size=128, hidden_size=64, intermediate_size=128, num_hidden_layers=2,
+                            num_attention_heads=4, num_key_value_heads=2, head_dim=16, max_position_embeddings=256)
+    torch.manual_seed(0)
+    model = Qwen3VLTextModel(cfg).eval()
+    patch.install_qwen3vl_triton_attention(model)
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(1, 128, (2, 12), generator=g)
+    mask = torch.ones((2, 12), dtype=torch.long)
+    mask[0, :5] = 0
+    ids[0, :5] = 0
+    steps = torch.randint(1, 128, (2, 3), generator=g)
+    outs = {}
+    for impl in ("sdpa", TEXT_BACKEND_KEY):
+        cfg._attn_implementation = impl
+        cache, m, res = DynamicCache(config=cfg), mask.clone(), []
+        with torch.no_grad():
+            res.append(model(input_ids=ids, attention_mask=m, past_key_values=cache).last_hidden_state[:, -1])
+            for s in range(steps.shape[1]):
+                m = torch.cat([m, torch.ones((2, 1), dtype=m.dtype)], 1)
+                res.append(model(input_ids=steps[:, s : s + 1], attention_mask=m,
+                                 past_key_values=cache).last_hidden_state[:, -1])
+        outs[impl] = torch.stack(res)
+    cfg._attn_implementation = "sdpa"
+    torch.testing.assert_close(outs[TEXT_BACKEND_KEY], outs["sdpa"], atol=1e-5, rtol=1e-5)
+
+
+def test_native_decode_entry_keeps_reference_checks():
+    """decode_q1_gqa_forward (dujunbaoV1/native_cuda_ops) refuses what the reference's TORCH_CHECKs refuse,
+    with RuntimeError, before anything reaches a device."""
+    from aicas_amd import native_ops
+
+    q, k = torch.zeros(1, 4, 64, dtype=torch.float16), torch.zeros(1, 2, 16, 64, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        native_ops.decode_q1_gqa_forward(q, k, k, 8, 0.125)
+    assert native_ops.is_available()

@@ -5,6 +5,8 @@ bitwise what DynamicLayer.update's torch.cat produces, see test_oracle.py), fp8_
 caches, paged_scatter_rows for paged caches.
 """
 
+import math
+
 import pytest
 import torch
 
@@ -192,3 +194,48 @@ def test_prefill_sized_append_many_sequences(dev, status):
     assert torch.equal(_bits(gv.cpu()), _bits(exp_v))
     assert pos.cpu().tolist() == new_lens
     assert int(status.item()) == 0
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("fused", [False, True])
+def test_fp8_non_finite_rows_are_stored_poisoned(dev, status, D, fused):
+    """Rows holding NaN, +Inf or -Inf reach an fp8 cache as the oracle stores them (scale NaN, all-zero codes)
+    and set AICAS_STATUS_NONFINITE_ROW; finite rows of the same launch are written code for code. Through the
+    fused append + attend, the sequence with a poisoned row attends to NaN (as the unquantised reference would),
+    the others are unaffected."""
+    B, H, G, cap = 4, 4, 2, 64
+    lens = [10, 20, 30, 40]
+    k_new = _rand((B, H, 1, D), 70 + D, scale=2.0).float()
+    v_new = _rand((B, H, 1, D), 71 + D, scale=2.0).float()
+    k_new[1, 2, 0, 5] = float("nan")
+    k_new[2, 0, 0, 0] = float("inf")
+    v_new[2, 3, 0, D - 1] = float("-inf")
+    k_new, v_new = k_new.to(torch.bfloat16), v_new.to(torch.bfloat16)
+    exp_kc, exp_ks = ref.fp8_quantize_rows(k_new[:, :, 0])
+    exp_vc, exp_vs = ref.fp8_quantize_rows(v_new[:, :, 0])
+    kc = torch.zeros((B, H, cap, D), dtype=torch.float8_e4m3fn, device=dev)
+    vc = torch.zeros_like(kc)
+    ks = torch.zeros((B, H, cap), dtype=torch.float32, device=dev)
+    vs = torch.zeros_like(ks)
+    view = ops.KVCacheView(kc, vc, ks, vs)
+    pos = torch.tensor(lens, dtype=torch.int32, device=dev)
+    if fused:
+        q = _rand((B, H * G, 1, D), 72).to(dev)
+        out = ops.decode_attention_append(q, view, k_new.to(dev), v_new.to(dev), pos, sm_scale=D ** -0.5,
+                                          max_seq_len=max(lens) + 1, status=status)
+    else:
+        ops.kv_append(view, k_new.to(dev), v_new.to(dev), pos, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) & _lib.STATUS_NONFINITE_ROW
+    for b, L in enumerate(lens):
+        got_k, got_v = kc[b, :, L].cpu().view(torch.uint8), vc[b, :, L].cpu().view(torch.uint8)
+        assert torch.equal(got_k, exp_kc[b].view(torch.uint8)) and torch.equal(got_v, exp_vc[b].view(torch.uint8))
+        torch.testing.assert_close(ks[b, :, L].cpu(), exp_ks[b], rtol=0, atol=0, equal_nan=True)
+        torch.testing.assert_close(vs[b, :, L].cpu(), exp_vs[b], rtol=0, atol=0, equal_nan=True)
+    assert math.isnan(float(ks[1, 2, lens[1]])) and math.isnan(float(ks[2, 0, lens[2]]))
+    assert math.isnan(float(vs[2, 3, lens[2]])) and not math.isnan(float(ks[0, 0, lens[0]]))
+    if fused:
+        o = out.float().cpu()
+        assert bool(torch.isnan(o[1, 2 * G : 3 * G]).all()) and bool(torch.isnan(o[2, 0:G]).all())
+        assert bool(torch.isnan(o[2, 3 * G : 4 * G]).all())  # a poisoned V row turns its heads' outputs NaN
+        assert bool(torch.isfinite(o[0]).all()) and bool(torch.isfinite(o[3]).all())

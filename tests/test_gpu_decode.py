@@ -345,3 +345,100 @@ def test_loose_bound_runs_the_tight_grid(dev, B, lens, cap):
     expect = ref.ragged_decode(q.cpu().float(), [kd[b, :, :lens[b]] for b in range(B)],
                                [vd[b, :, :lens[b]] for b in range(B)], D ** -0.5, G).float()
     torch.testing.assert_close(loose.float().cpu(), expect, atol=2e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("page", [1, 2])
+@pytest.mark.parametrize("fused", [False, True])
+def test_paged_range_mode(dev, status, fp8, page, fused):
+    """Paged rows longer than the kernel's LDS block-id cache (2048 entries: here 1- and 2-token pages with
+    lengths up to 5000) are streamed as one static token range per split, each split staging only its range's
+    block ids. A randomly permuted block table with one invalid entry (its page is skipped and reported); plain
+    decode and the fused append + attend, bf16 and fp8, against the oracle over the gathered pages."""
+    gen = torch.Generator().manual_seed(400 + 10 * page + 2 * fp8 + fused)
+    B, Hkv, G, D = 3, 8, 2, 128
+    lens = [2100 * page + 1, 4999, 1500 * page + 777]
+    assert max(-(-L // page) for L in lens) > 2048
+    per_seq = [-(-(L + 1) // page) for L in lens]
+    nblocks = sum(per_seq) + 7
+    perm = torch.randperm(nblocks, generator=gen).to(torch.int32)
+    bt = torch.full((B, max(per_seq)), -1, dtype=torch.int32)
+    at = 0
+    for b, n in enumerate(per_seq):
+        bt[b, :n] = perm[at : at + n]
+        at += n
+    bad_b, bad_page = 1, 1234 // page  # one invalid entry inside sequence 1: its tokens are skipped
+    bt[bad_b, bad_page] = -5
+    kv_dtype = ops.FP8_DTYPE if fp8 else torch.bfloat16
+    src_k = _rand((nblocks, Hkv, page, D), gen)
+    src_v = _rand((nblocks, Hkv, page, D), gen)
+    if fp8:
+        ck, sk = ref.fp8_quantize_rows(src_k)
+        cv, sv = ref.fp8_quantize_rows(src_v)
+        view = ops.KVCacheView(ck.to(dev), cv.to(dev), sk.to(dev), sv.to(dev), bt.to(dev))
+    else:
+        view = ops.KVCacheView(src_k.to(dev), src_v.to(dev), block_table=bt.to(dev))
+    q = _rand((B, Hkv * G, 1, D), gen).to(dev)
+    pos = torch.tensor(lens, dtype=torch.int32, device=dev)
+    if fused:
+        kn, vn = _rand((B, Hkv, 1, D), gen).to(dev), _rand((B, Hkv, 1, D), gen).to(dev)
+        out = ops.decode_attention_append(q, view, kn, vn, pos, sm_scale=D ** -0.5, max_seq_len=max(lens) + 1,
+                                          seq_lens_out=pos, status=status)
+        full = [L + 1 for L in lens]
+    else:
+        out = ops.decode_attention(q, view, sm_scale=D ** -0.5, seq_lens=pos, max_seq_len=max(lens), status=status)
+        full = list(lens)
+    torch.cuda.synchronize()
+    assert int(status.item()) & _lib.STATUS_BLOCK_OUT_OF_RANGE
+    if fused:
+        assert pos.cpu().tolist() == full
+    # the oracle: every valid page gathered from the pool as the kernel leaves it, the invalid page's tokens
+    # dropped, then per-sequence attention
+    table = ref.e4m3_decode_table()
+    cpu_bt = bt.clamp(min=0)
+    ks, vs = [], []
+    for b, L in enumerate(full):
+        if fp8:
+            k = ref.paged_gather(view.k.cpu().view(torch.uint8), cpu_bt[b : b + 1], [L])[0]
+            v = ref.paged_gather(view.v.cpu().view(torch.uint8), cpu_bt[b : b + 1], [L])[0]
+            k = table[k.long()] * ref.paged_gather(view.k_scale.cpu(), cpu_bt[b : b + 1], [L])[0][..., None]
+            v = table[v.long()] * ref.paged_gather(view.v_scale.cpu(), cpu_bt[b : b + 1], [L])[0][..., None]
+        else:
+            k = ref.paged_gather(view.k.cpu(), cpu_bt[b : b + 1], [L])[0].float()
+            v = ref.paged_gather(view.v.cpu(), cpu_bt[b : b + 1], [L])[0].float()
+        keep = torch.ones(L, dtype=torch.bool)
+        if b == bad_b:
+            keep[bad_page * page : (bad_page + 1) * page] = False
+        ks.append(k[:, keep])
+        vs.append(v[:, keep])
+    expect = ref.ragged_decode(q.cpu().float(), ks, vs, D ** -0.5, G, fp64=True)
+    err = float((out.double().cpu() - expect).abs().max())
+    assert err <= (ATOL_FP8 if fp8 else ATOL_16), err
+    if fused and not fp8:
+        for b, L in enumerate(lens):  # the appended rows landed in their pages
+            blk, row = int(bt[b, L // page]), L % page
+            assert torch.equal(view.k[blk, :, row].cpu().view(torch.int16), kn[b, :, 0].cpu().view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("B, Hq, Hkv, D, cap, visible", [(1, 16, 8, 128, 1024, 700), (4, 16, 8, 128, 4096, 4096),
+                                                         (2, 8, 2, 64, 65, 65), (1, 16, 4, 128, 8192, 8000)])
+def test_native_decode_entry(dev, dtype, B, Hq, Hkv, D, cap, visible):
+    """decode_q1_gqa_forward, the drop-in for dujunbaoV1's native op: [B, Hq, D] out of a fixed-capacity cache
+    attended to its first visible_len tokens, against the oracle; and the reference's argument checks."""
+    from aicas_amd import native_ops
+
+    gen = torch.Generator().manual_seed(B * 1000 + cap)
+    q = _rand((B, Hq, D), gen, dtype)
+    k = _rand((B, Hkv, cap, D), gen, dtype)
+    v = _rand((B, Hkv, cap, D), gen, dtype)
+    out = native_ops.decode_q1_gqa_forward(q.to(dev), k.to(dev), v.to(dev), visible, D ** -0.5)
+    assert out.shape == (B, Hq, D) and out.dtype == dtype
+    expect = ref.sdpa_decode(q[:, :, None].float(), k[:, :, :visible].float(), v[:, :, :visible].float(),
+                             D ** -0.5, Hq // Hkv)[:, :, 0]
+    torch.testing.assert_close(out.float().cpu(), expect, atol=ATOL_16, rtol=1e-2)
+    for bad_len in (0, cap + 1):
+        with pytest.raises(RuntimeError, match="visible_len"):
+            native_ops.decode_q1_gqa_forward(q.to(dev), k.to(dev), v.to(dev), bad_len, D ** -0.5)
+    with pytest.raises(RuntimeError, match="contiguous"):
+        native_ops.decode_q1_gqa_forward(q.to(dev), k.to(dev).transpose(2, 3), v.to(dev), visible, D ** -0.5)

@@ -151,3 +151,48 @@ def test_golden_fp8_rows_quantize_on_write(dev):
     assert torch.equal(view.k[:, 0, 2].cpu().view(torch.uint8), FIX["fp8.rows_codes"])
     assert torch.equal(view.v[:, 0, 2].cpu().view(torch.uint8), FIX["fp8.rows_codes"])
     assert torch.equal(view.k_scale[:, 0, 2].cpu(), FIX["fp8.rows_scale"])
+
+
+@pytest.mark.parametrize("kv_dtype, page_size", [(None, None), (torch.float8_e4m3fn, None), (None, 16)])
+def test_left_padded_batch(dev, kv_dtype, page_size):
+    """A left-padded batch (HF hands the attention function its 2-D padding mask): a dense bf16 aicas cache gives
+    HF's DynamicCache + SDPA hidden states (the masked calls take the SDPA route with HF's own 4-D mask); an fp8 or
+    paged cache, which only the decode kernel can read and which has no per-token mask, refuses the first masked
+    decode step with a ValueError instead of attending to the pad tokens."""
+    from transformers.cache_utils import DynamicCache
+
+    model, cfg = _model(dev)
+    patch.install_qwen3vl_triton_attention(model)
+    g = torch.Generator().manual_seed(9)
+    ids = torch.randint(1, 512, (3, 40), generator=g)
+    mask = torch.ones((3, 40), dtype=torch.long)
+    for b, pad in enumerate((7, 0, 19)):
+        ids[b, :pad] = 0
+        mask[b, :pad] = 0
+    ids, mask = ids.to(dev), mask.to(dev)
+    steps = torch.randint(1, 512, (3, 4), generator=g).to(dev)
+
+    def run(impl, cache):
+        cfg._attn_implementation = impl
+        m, res = mask.clone(), []
+        try:
+            with torch.no_grad():
+                res.append(model(input_ids=ids, attention_mask=m, past_key_values=cache).last_hidden_state[:, -1])
+                for s in range(steps.shape[1]):
+                    m = torch.cat([m, torch.ones((3, 1), dtype=m.dtype, device=dev)], 1)
+                    res.append(model(input_ids=steps[:, s : s + 1], attention_mask=m,
+                                     past_key_values=cache).last_hidden_state[:, -1])
+        finally:
+            cfg._attn_implementation = "sdpa"
+        return res
+
+    ref_outs = run("sdpa", DynamicCache(config=cfg))
+    cache = AicasDecodeCache(num_layers=cfg.num_hidden_layers, max_cache_len=64, kv_dtype=kv_dtype,
+                             page_size=page_size)
+    if kv_dtype is None and page_size is None:
+        outs = run(TEXT_BACKEND_KEY, cache)
+        for a, b in zip(outs, ref_outs):
+            assert _rel(a, b) < 3e-2
+    else:
+        with pytest.raises(ValueError, match="padding mask"):
+            run(TEXT_BACKEND_KEY, cache)

@@ -211,6 +211,25 @@ def test_fp8_quantize_rows_properties():
     assert bool((err <= bound).all())
 
 
+def test_fp8_quantize_rows_poisons_non_finite_rows():
+    """A row holding NaN or +-Inf (anywhere, any sign) is stored poisoned: scale NaN, every code 0, so that it
+    dequantises to NaN everywhere; finite rows in the same call are quantized as on their own."""
+    x = _bf16((6, 32), 48, scale=2.0).float()
+    finite_rows = x[[0, 5]].clone()
+    x[1, 3] = float("nan")
+    x[2, 0] = float("inf")
+    x[3, 31] = float("-inf")
+    x[4, :] = float("nan")
+    codes, scale = ref.fp8_quantize_rows(x)
+    for r in (1, 2, 3, 4):
+        assert math.isnan(float(scale[r]))
+        assert torch.count_nonzero(codes[r].view(torch.uint8)) == 0
+        assert bool(torch.isnan(ref.fp8_dequantize_rows(codes[r : r + 1], scale[r : r + 1])).all())
+    c0, s0 = ref.fp8_quantize_rows(finite_rows)
+    assert torch.equal(codes[[0, 5]].view(torch.uint8), c0.view(torch.uint8)) and torch.equal(scale[[0, 5]], s0)
+    assert torch.equal(s0, finite_rows.abs().amax(dim=-1) / 448.0)
+
+
 # ------------------------------------------------------------------------------------------- LSE merge
 @pytest.mark.parametrize("splits", [[0, 100], [0, 1, 100], [0, 37, 64, 99, 100], list(range(0, 101, 10))])
 def test_lse_merge_equals_single_pass(splits):
