@@ -24,6 +24,9 @@ SOURCES = [
 ]
 INCLUDE = os.path.join(os.path.dirname(PKG_DIR), "include")
 OUTPUT = os.path.join(PKG_DIR, "libaicas_decode.so")
+# bandwidth calibration kernels for bench.py --config calib (a library of their own, outside the decode ABI)
+CALIB_SOURCES = [os.path.join(CSRC, "calib.hip")]
+CALIB_OUTPUT = os.path.join(PKG_DIR, "libaicas_calib.so")
 OBJ_DIR = os.path.join(PKG_DIR, "_build")
 ARCH = "gfx950"
 
@@ -66,19 +69,23 @@ def _run(cmd: list[str], verbose: bool) -> None:
 
 
 def build(verbose: bool = True, sources: list[str] | None = None, output: str = OUTPUT,
-          include: str = INCLUDE, obj_dir: str = OBJ_DIR) -> str:
-    """Compile every translation unit in parallel and link the library in-tree (always recompiles)."""
+          include: str = INCLUDE, obj_dir: str = OBJ_DIR, calib: bool = True) -> str:
+    """Compile every translation unit in parallel and link the library in-tree (always recompiles); with calib
+    (the default build), also the calibration library libaicas_calib.so."""
     from concurrent.futures import ThreadPoolExecutor
 
     sources = sources or SOURCES
+    libs = [(list(sources), output)] + ([(CALIB_SOURCES, CALIB_OUTPUT)] if calib else [])
     os.makedirs(obj_dir, exist_ok=True)
-    objs = [os.path.join(obj_dir, os.path.splitext(os.path.basename(src))[0] + ".o") for src in sources]
-    jobs = max(1, min(len(sources), os.cpu_count() or 1, 8))
+    obj = lambda src: os.path.join(obj_dir, os.path.splitext(os.path.basename(src))[0] + ".o")  # noqa: E731
+    units = [src for srcs, _ in libs for src in srcs]
+    jobs = max(1, min(len(units), os.cpu_count() or 1, 8))
     with ThreadPoolExecutor(jobs) as pool:
-        list(pool.map(lambda so: _run(compile_command(so[0], so[1], include), verbose), zip(sources, objs)))
-    tmp = output + ".tmp"
-    _run(link_command(objs, tmp), verbose)
-    os.replace(tmp, output)
+        list(pool.map(lambda src: _run(compile_command(src, obj(src), include), verbose), units))
+    for srcs, out in libs:
+        tmp = out + ".tmp"
+        _run(link_command([obj(src) for src in srcs], tmp), verbose)
+        os.replace(tmp, out)
     return output
 
 

@@ -1,0 +1,101 @@
+// Bandwidth calibration kernels for bench.py --config calib (libaicas_calib.so; not part of the decode ABI).
+//
+// They read exactly the bytes one decode launch of a contiguous bf16 cache reads (K and V rows of B sequences x
+// Hkv heads x L tokens, head_dim 128) and compute nothing but an xor of the words, so that their time is the
+// streaming ceiling the attention launch is compared with:
+//   aicas_calib_stream_read  the attention's own grid and access pattern: (splits, Hkv, B) workgroups of 4 waves,
+//                            the sequence's 32-token super-chunks dealt round-robin to its 4 * splits waves, each
+//                            super-chunk 2 x 4 non-temporal 16-byte loads of K and of V per lane;
+//   aicas_calib_flat_read    the same bytes as one flat range per tensor in `blocks` workgroups (grid-stride,
+//                            16 bytes per lane per load): what a finely balanced plain read achieves;
+//   aicas_calib_empty        an empty launch (dispatch and completion cost).
+// Every thread stores its xor to `sink`, so no load is dead.
+
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include "common.hpp"
+
+namespace {
+
+constexpr int kD = 128;          // head_dim
+constexpr int kLanesPerRow = 16; // 16 bytes per lane per bf16 row of 128
+constexpr int kRowsPerLoad = aicas::kWave / kLanesPerRow;
+constexpr int kChunk = 4 * kRowsPerLoad;  // tokens per wave chunk (4 loads)
+constexpr int kSuper = 2 * kChunk;        // tokens per super-chunk
+
+__device__ __forceinline__ uint32_t fold(uint4 w) { return w.x ^ w.y ^ w.z ^ w.w; }
+
+__global__ __launch_bounds__(aicas::kBlockThreads) void stream_read_kernel(const uint16_t* k, const uint16_t* v,
+                                                                          int64_t stride_b, int64_t stride_h, int L,
+                                                                          uint32_t* sink) {
+  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / aicas::kWave);
+  const int lane = threadIdx.x % aicas::kWave;
+  const int row = lane / kLanesPerRow, li = lane % kLanesPerRow;
+  const int stripe = gridDim.x * aicas::kWavesPerBlock;
+  const int n_super = (L + kSuper - 1) / kSuper;
+  const int64_t base = b * stride_b + h * stride_h + li * 8;
+  uint32_t acc = 0;
+  for (int j = split * aicas::kWavesPerBlock + wave; j < n_super; j += stripe) {
+    uint4 kw[8], vw[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int t = min(j * kSuper + u * kRowsPerLoad + row, L - 1);
+      kw[u] = aicas::load_stream16(k + base + static_cast<int64_t>(t) * kD);
+      vw[u] = aicas::load_stream16(v + base + static_cast<int64_t>(t) * kD);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc ^= fold(kw[u]) ^ fold(vw[u]);
+  }
+  sink[((static_cast<int64_t>(b) * gridDim.y + h) * gridDim.x + split) * blockDim.x + threadIdx.x] = acc;
+}
+
+__global__ __launch_bounds__(aicas::kBlockThreads) void flat_read_kernel(const uint4* k, const uint4* v, int64_t n16,
+                                                                        uint32_t* sink) {
+  uint32_t acc = 0;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n16; i += 2 * stride) {
+    const uint4 a = aicas::load_stream16(k + i), c = aicas::load_stream16(v + i);
+    uint4 a2 = make_uint4(0, 0, 0, 0), c2 = a2;
+    if (i + stride < n16) {
+      a2 = aicas::load_stream16(k + i + stride);
+      c2 = aicas::load_stream16(v + i + stride);
+    }
+    acc ^= fold(a) ^ fold(c) ^ fold(a2) ^ fold(c2);
+  }
+  sink[static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x] = acc;
+}
+
+__global__ void empty_kernel() {}
+
+}  // namespace
+
+extern "C" {
+
+// k, v: [B, Hkv, capacity, 128] bf16 (element strides stride_b, stride_h; token stride 128); reads the first L
+// tokens of every (b, h). sink: splits * Hkv * B * 256 words.
+int aicas_calib_stream_read(const void* k, const void* v, int64_t stride_b, int64_t stride_h, int32_t batch,
+                            int32_t num_kv_heads, int32_t L, int32_t splits, uint32_t* sink, hipStream_t stream) {
+  if (!k || !v || !sink || batch <= 0 || num_kv_heads <= 0 || L <= 0 || splits <= 0) return 1;
+  hipLaunchKernelGGL(stream_read_kernel, dim3(splits, num_kv_heads, batch), dim3(aicas::kBlockThreads), 0, stream,
+                     static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), stride_b, stride_h, L, sink);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+// k, v: contiguous buffers of n_bytes each (a multiple of 16). sink: blocks * 256 words.
+int aicas_calib_flat_read(const void* k, const void* v, int64_t n_bytes, int32_t blocks, uint32_t* sink,
+                          hipStream_t stream) {
+  if (!k || !v || !sink || n_bytes <= 0 || (n_bytes % 16) || blocks <= 0) return 1;
+  hipLaunchKernelGGL(flat_read_kernel, dim3(blocks), dim3(aicas::kBlockThreads), 0, stream,
+                     static_cast<const uint4*>(k), static_cast<const uint4*>(v), n_bytes / 16, sink);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+int aicas_calib_empty(hipStream_t stream) {
+  hipLaunchKernelGGL(empty_kernel, dim3(1), dim3(64), 0, stream);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+}  // extern "C"

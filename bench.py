@@ -61,7 +61,7 @@ MALL_BYTES = 256 << 20
 def parse_args(argv=None):
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--config", choices=("c1", "c2", "c3", "c4", "c5", "model", "microbench"), default="c2",
+    p.add_argument("--config", choices=("c1", "c2", "c3", "c4", "c5", "model", "microbench", "calib"), default="c2",
                    help="model: the whole text-decoder step per generated token; microbench: the shape of the "
                         "reference's published decode microbenchmark (both reported separately)")
     p.add_argument("--prompt-len", type=int, default=1024, help="model: cached tokens before the timed steps")
@@ -84,6 +84,9 @@ def parse_args(argv=None):
     p.add_argument("--compare-qk", type=int, default=1,
                    help="also time the fused path with the q/k RMSNorm + rotary prologue (reported, not the value)")
     p.add_argument("--tokens-per-split", type=int, default=0, help="0 = the library's plan")
+    p.add_argument("--cache-instances", type=int, default=0,
+                   help="one-layer configurations: cache instances stepped through (0: enough to exceed twice the "
+                        "256 MB memory-side cache, at least 4; 1 lets that cache serve the reads)")
     p.add_argument("--cpu-baseline-seconds", type=float, default=15.0,
                    help="approximate CPU time budget for the oracle baseline (0 disables it)")
     p.add_argument("--kernel-timing-steps", type=int, default=8,
@@ -388,12 +391,123 @@ def microbench(args) -> int:
     return 0
 
 
+def calib(args) -> int:
+    """--config calib: the per-launch streaming ceiling the headline launch is measured against, from committed
+    code. One layer of the headline workload (B=8, 8 kv heads, head_dim 128, 2112 tokens: the mean length of a
+    128-step run, 69.2 MB of K and V) is read by, per launch: the fused append + attend launch itself; a pure
+    streaming read with the attention's grid and access pattern (libaicas_calib.so, at the plan's 4 splits per
+    (batch, kv head) pair and at 8); a flat read of the same bytes in 4096 workgroups; and an empty launch. 28
+    distinct layers (1.9 GB) are launched back to back in a graph, so the 256 MB memory-side cache cannot serve
+    the reads; µs per launch = graph time / launches."""
+    import ctypes
+
+    import torch
+
+    from aicas_amd import ops
+    from aicas_amd.build import CALIB_OUTPUT
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    B, HQ, HKV, D, L, NL = 8, 16, 8, 128, 2112, 28
+    reps = args.steps or 20
+    lib = ctypes.CDLL(CALIB_OUTPUT, mode=ctypes.RTLD_LOCAL)
+    P, I32, I64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    lib.aicas_calib_stream_read.argtypes = [P, P, I64, I64, I32, I32, I32, I32, P, P]
+    lib.aicas_calib_flat_read.argtypes = [P, P, I64, I32, P, P]
+    lib.aicas_calib_empty.argtypes = [P]
+    gen = torch.Generator(device=dev).manual_seed(2)
+    ks = [torch.randn((B, HKV, L + 1, D), generator=gen, device=dev).to(torch.bfloat16) for _ in range(NL)]
+    vs = [torch.randn((B, HKV, L + 1, D), generator=gen, device=dev).to(torch.bfloat16) for _ in range(NL)]
+    q = torch.randn((NL, B, HQ, 1, D), generator=gen, device=dev).to(torch.bfloat16)
+    kn = torch.randn((NL, B, HKV, 1, D), generator=gen, device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    pos = torch.full((B,), L - 1, dtype=torch.int32, device=dev)  # attend over L tokens, the last one appended
+    plan = ops.decode_plan(torch.bfloat16, B, HQ, HKV, D, L)
+    ws = ops.Workspace.reserve(dev, plan.workspace_bytes)
+    sink = torch.empty(4096 * 256, dtype=torch.int32, device=dev)
+    kv_bytes = 2 * B * HKV * L * D * 2
+    stream = torch.cuda.Stream(device=dev)
+
+    def check(rc):
+        if rc:
+            raise RuntimeError(f"calibration launch failed ({rc})")
+
+    def attention(i):
+        ops.decode_attention_append(q[i], ops.KVCacheView(ks[i], vs[i]), kn[i], kn[i], pos, sm_scale=D ** -0.5,
+                                    max_seq_len=L, min_seq_len=L - 1, out=out[i], workspace=ws)
+
+    def stream_read(splits):
+        return lambda i: check(lib.aicas_calib_stream_read(ks[i].data_ptr(), vs[i].data_ptr(), ks[i].stride(0),
+                                                           ks[i].stride(1), B, HKV, L, splits, sink.data_ptr(),
+                                                           stream.cuda_stream))
+
+    # the flat read covers each tensor's first B*Hkv*(L+1)*D elements: the L attended tokens plus one row per
+    # (batch, kv head) pair, 0.05% more bytes, counted
+    flat_bytes = ks[0].numel() * 2
+
+    def flat_read(i):
+        check(lib.aicas_calib_flat_read(ks[i].data_ptr(), vs[i].data_ptr(), flat_bytes, 4096, sink.data_ptr(),
+                                        stream.cuda_stream))
+
+    def empty(i):
+        check(lib.aicas_calib_empty(stream.cuda_stream))
+
+    def per_launch_us(fn):
+        with torch.cuda.stream(stream):
+            for i in range(NL):
+                fn(i)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                for i in range(NL):
+                    fn(i)
+            for _ in range(3):
+                graph.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (reps * NL)
+
+    rows = {}
+    for name, fn, nbytes in (
+        ("fused append + attend launch (the headline kernel)", attention, algorithmic_bytes(B, HQ, HKV, D, [L] * B)),
+        (f"streaming read, the attention's grid ({plan.num_splits} splits x 64 pairs)", stream_read(plan.num_splits),
+         kv_bytes),
+        ("streaming read, the attention's pattern at 8 splits", stream_read(8), kv_bytes),
+        ("flat read of the same bytes, 4096 workgroups", flat_read, 2 * flat_bytes),
+        ("empty launch", empty, 0),
+    ):
+        us = per_launch_us(fn)
+        rows[name] = {"us_per_launch": round(us, 3), "bytes": nbytes,
+                      "gbps": round(nbytes / (us * 1e-6) / 1e9, 1) if nbytes else None,
+                      "frac_of_8tbps": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4) if nbytes else None}
+        print(f"[calib] {name}: {us:.3f} us per launch", file=sys.stderr, flush=True)
+    result = {
+        "metric": "us per launch: the headline launch against pure streaming reads of the same bytes and an empty "
+                  "launch (calibration, reported beside the headline, not the headline)",
+        "value": rows["fused append + attend launch (the headline kernel)"]["us_per_launch"], "unit": "us/launch",
+        "n_gpus": 1, "steps": reps, "warmup": 3, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (seeded N(0,1))",
+        "config": {"workload": f"one layer of the B=8 decode step: 8 kv heads, head_dim 128, {L} tokens, {NL} "
+                               "distinct layers per graph", "batch": B, "tokens": L, "splits": plan.num_splits},
+        "launches": rows,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.config == "model" and args.gpus == 1:
         return model_step(args)
     if args.config == "microbench" and args.gpus == 1:
         return microbench(args)
+    if args.config == "calib" and args.gpus == 1:
+        return calib(args)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: each GPU serves its own "
               "sequences (or kv heads), so the step does not shard across GPUs here.", file=sys.stderr)
@@ -421,6 +535,8 @@ def main(argv=None) -> int:
     # twice the MALL (>= 4), stepped through in turn within each step
     one_layer = algorithmic_bytes(B, HQ, HKV, D, [L + n_graph_steps for L in base], w.fp8, page)
     NL = w.layers if w.layers > 1 else max(4, math.ceil(2 * MALL_BYTES / one_layer))
+    if w.layers == 1 and args.cache_instances > 0:
+        NL = args.cache_instances
     layer_weight = w.layers / NL  # one-layer configs: a step's time is the per-layer time
     cap_seq = max(base) + n_graph_steps
 
