@@ -27,7 +27,9 @@
 // and bumps the (b, kv head) arrival counter. The split that arrives last reads every split's partial with
 // agent-scope loads and combines them: M = max m_i, l = sum l_i 2^(m_i - M), out = sum acc_i 2^(m_i - M) / l;
 // it then re-arms the counter to zero. Nothing ever waits on another workgroup. Sequences that need one
-// split write the output directly.
+// split write the output directly. Up to 8 splits the merging workgroup reads one output cell per thread; above
+// that it reads the partials in 16-byte pieces, several threads per group of 4 cells, so that its loads stay
+// one or two round trips deep.
 //
 // Prologue: q, the new rows (APPEND) and the q/k preparation's inputs, weights and rotary rows (QK) are fetched
 // before the lengths are read, so that their latencies overlap; every wave reads its sequence's length with a
@@ -121,6 +123,9 @@ __device__ __forceinline__ void store_agent(float* p, float v) {
 __device__ __forceinline__ float load_agent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Cache-policy operand of the buffer-load builtin that sets sc1: the bit a relaxed agent-scope atomic load
+// carries (global_load_dword ... sc1), here on 16-byte loads.
+constexpr int kAuxSc1 = 16;
 
 // The model's q/k preparation for one pair of adjacent elements (d0, d0 + 1) of a head row whose D/2 pairs are
 // held by D/2 consecutive lanes of one wave (every lane of the row must take part): RMSNorm over head_dim in
@@ -203,7 +208,10 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
 
   __shared__ float s_m[kWavesPerBlock][G];
   __shared__ float s_l[kWavesPerBlock][G];
-  __shared__ float s_acc[kWavesPerBlock][G][D];
+  // the 4 waves' accumulators; later, in the workgroup that merges many splits, the merge's per-thread states
+  constexpr int kPoolFloats = kWavesPerBlock * G * D > 6 * kBlockThreads ? kWavesPerBlock * G * D : 6 * kBlockThreads;
+  __shared__ __align__(16) float s_pool[kPoolFloats];
+  auto& s_acc = *reinterpret_cast<float (*)[kWavesPerBlock][G][D]>(s_pool);
   __shared__ int32_t s_bt[PAGED ? kMaxBlockEntries : 1];
   __shared__ int32_t s_last;
   // APPEND: the new token's rows as the attention must see them (dequantised codes for fp8 caches)
@@ -826,6 +834,8 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   }
 
   uint16_t* outb = static_cast<uint16_t*>(p.out) + b * p.out_stride_b;
+  // QK: the prepared q goes out from the workgroup that writes the output, after every split of the pair has
+  // read q (q_out may be q itself)
   auto write_out = [&](const float* ls, const float* a) {
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
@@ -836,8 +846,6 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
         outb[hq * p.out_stride_h + idx % D] = from_f32<Q_DT>(ls[c] == 0.0f ? 0.0f : a[c] / ls[c]);
       }
     }
-    // QK: the prepared q goes out from the workgroup that writes the output, after every split of the pair has
-    // read q (q_out may be q itself)
     if constexpr (QK) {
       if (p.q_out) {
         for (int pp = tid; pp < G * (D / 2); pp += kBlockThreads) {
@@ -884,64 +892,140 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
     return;
   }
 
-  // One online pass over the splits in order, a batch of MB splits at a time for all of this thread's cells: the
-  // batch's loads are issued unconditionally (past the last split they repeat it, masked below), so they are in
-  // flight together and the merge costs ceil(n_active / MB) memory round trips; loads behind per-split branches
-  // would each end in a wait of their own. A batch keeps at most 48 loads in flight per thread: 16 splits for one
-  // cell (8 when at most 8 splits exist, so that few repeats go out), 8 for two cells, 4 for four.
+  // The last arriver combines the n_active partials, in split order for every output cell.
   float rl[CPT], ra[CPT];
-  auto merge_all = [&](auto mb_tag) {
-    constexpr int MB = decltype(mb_tag)::value;
-    float M[CPT], ls[CPT], a[CPT];
-    int64_t hbase[CPT];
-    int dcol[CPT];
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int idx = min(tid + c * kBlockThreads, G * D - 1);
-      hbase[c] = pair_base + (idx / D) * p.max_splits;
-      dcol[c] = idx % D;
-      M[c] = kNegBig;
-      ls[c] = 0.0f;
-      a[c] = 0.0f;
-    }
-    for (int i0 = 0; i0 < n_active; i0 += MB) {
-      float mi[CPT][MB], li[CPT][MB], ai[CPT][MB];
+  if (n_active <= 8) {
+    // Few splits: one (head, d) cell per thread and round, a batch of MB splits at a time for all of the thread's
+    // cells: the batch's loads are issued unconditionally (past the last split they repeat it, masked below), so
+    // they are in flight together and the merge costs ceil(n_active / MB) memory round trips (one unless a
+    // thread has four cells); loads behind per-split branches would each end in a wait of their own.
+    auto merge_cells = [&](auto mb_tag) {
+      constexpr int MB = decltype(mb_tag)::value;
+      float M[CPT], ls[CPT], a[CPT];
+      int64_t hbase[CPT];
+      int dcol[CPT];
 #pragma unroll
       for (int c = 0; c < CPT; ++c) {
-#pragma unroll
-        for (int j = 0; j < MB; ++j) {
-          const int i = min(i0 + j, n_active - 1);
-          mi[c][j] = load_agent(p.ws_ml + 2 * (hbase[c] + i));
-          li[c][j] = load_agent(p.ws_ml + 2 * (hbase[c] + i) + 1);
-          ai[c][j] = load_agent(p.ws_acc + (hbase[c] + i) * D + dcol[c]);
-        }
+        const int idx = min(tid + c * kBlockThreads, G * D - 1);
+        hbase[c] = pair_base + (idx / D) * p.max_splits;
+        dcol[c] = idx % D;
+        M[c] = kNegBig;
+        ls[c] = 0.0f;
+        a[c] = 0.0f;
       }
+      for (int i0 = 0; i0 < n_active; i0 += MB) {
+        float mi[CPT][MB], li[CPT][MB], ai[CPT][MB];
 #pragma unroll
-      for (int c = 0; c < CPT; ++c) {
+        for (int c = 0; c < CPT; ++c) {
 #pragma unroll
-        for (int j = 0; j < MB; ++j) {
-          if (i0 + j < n_active) {
-            const float mn = fmaxf(M[c], mi[c][j]);
-            const float c_old = fast_exp2(M[c] - mn);
-            const float c_new = fast_exp2(mi[c][j] - mn);
-            ls[c] = ls[c] * c_old + li[c][j] * c_new;
-            a[c] = a[c] * c_old + ai[c][j] * c_new;
-            M[c] = mn;
+          for (int j = 0; j < MB; ++j) {
+            const int i = min(i0 + j, n_active - 1);
+            mi[c][j] = load_agent(p.ws_ml + 2 * (hbase[c] + i));
+            li[c][j] = load_agent(p.ws_ml + 2 * (hbase[c] + i) + 1);
+            ai[c][j] = load_agent(p.ws_acc + (hbase[c] + i) * D + dcol[c]);
+          }
+        }
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+#pragma unroll
+          for (int j = 0; j < MB; ++j) {
+            if (i0 + j < n_active) {
+              const float mn = fmaxf(M[c], mi[c][j]);
+              const float c_old = fast_exp2(M[c] - mn);
+              const float c_new = fast_exp2(mi[c][j] - mn);
+              ls[c] = ls[c] * c_old + li[c][j] * c_new;
+              a[c] = a[c] * c_old + ai[c][j] * c_new;
+              M[c] = mn;
+            }
           }
         }
       }
-    }
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) {
+        rl[c] = ls[c];
+        ra[c] = a[c];
+      }
+    };
+    merge_cells(std::integral_constant<int, (CPT >= 4 ? 4 : 8)>{});
+  } else {
+    // Many splits: the partials' acc rows are read in 16-byte pieces. Thread t takes the 4 accumulator columns of
+    // cell quad t % Q (Q = G * D / 4 quads: a head and 4 consecutive d) for the splits t / Q, t / Q + S, ...
+    // (S = 256 / Q threads per quad): one 16-byte acc load and one 8-byte (m, l) load per split, both
+    // agent-scope, a batch of MB of its splits at a time (issued unconditionally, as above), so the merge costs
+    // ceil(ceil(n_active / S) / MB) memory round trips. Each thread combines its splits in order; the S states
+    // of a quad are then combined in sub order through LDS.
+    constexpr int Q = G * D / 4;
+    constexpr int S = kBlockThreads / Q;
+    static_assert(Q * 4 == G * D && S * Q == kBlockThreads, "cell quads must tile the workgroup");
+    const int quad = tid % Q;
+    const int sub = tid / Q;  // uniform across a wave whenever Q >= 64
+    const int qh = quad / (D / 4);
+    const auto acc_rsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_acc + pair_base * D, static_cast<short>(0),
+                                                            0x7fffffff, 0x00020000);
+    const uint64_t* const ml_base =
+        reinterpret_cast<const uint64_t*>(p.ws_ml + 2 * (pair_base + static_cast<int64_t>(qh) * p.max_splits));
+    const int acc_off = (qh * p.max_splits * D + (quad % (D / 4)) * 4) * 4;  // bytes, split 0
+    float wm = kNegBig, wl = 0.0f, wa[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto merge_quads = [&](auto mb_tag) {
+      constexpr int MB = decltype(mb_tag)::value;
+      for (int i0 = sub; i0 < n_active; i0 += MB * S) {
+        float4 ai[MB];
+        uint64_t mli[MB];
+#pragma unroll
+        for (int j = 0; j < MB; ++j) {
+          const int i = min(i0 + j * S, n_active - 1);
+          ai[j] = __builtin_bit_cast(
+              float4, __builtin_amdgcn_raw_buffer_load_b128(acc_rsrc, acc_off + i * D * 4, 0, kAuxSc1));
+          mli[j] = __hip_atomic_load(const_cast<uint64_t*>(ml_base) + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int j = 0; j < MB; ++j) {
+          if (i0 + j * S < n_active) {
+            const float mi = __uint_as_float(static_cast<uint32_t>(mli[j]));
+            const float li = __uint_as_float(static_cast<uint32_t>(mli[j] >> 32));
+            const float mn = fmaxf(wm, mi);
+            const float c_old = fast_exp2(wm - mn);
+            const float c_new = fast_exp2(mi - mn);
+            wl = wl * c_old + li * c_new;
+            wa[0] = wa[0] * c_old + ai[j].x * c_new;
+            wa[1] = wa[1] * c_old + ai[j].y * c_new;
+            wa[2] = wa[2] * c_old + ai[j].z * c_new;
+            wa[3] = wa[3] * c_old + ai[j].w * c_new;
+            wm = mn;
+          }
+        }
+      }
+    };
+    // batch: the thread's split count rounded up to a power of two, from 4 to 16 (96 registers of loads)
+    const int per_thread = (n_active + S - 1) / S;
+    if (per_thread > 8) merge_quads(std::integral_constant<int, 16>{});
+    else if (per_thread > 4) merge_quads(std::integral_constant<int, 8>{});
+    else merge_quads(std::integral_constant<int, 4>{});
+    // LDS (the wave-merge area: every thread is past its last read of it): [thread] (m, l), then [thread] acc
+    // quad; thread sub * Q + quad holds sub's state of the quad
+    s_pool[2 * tid] = wm;
+    s_pool[2 * tid + 1] = wl;
+    reinterpret_cast<float4*>(s_pool + 2 * kBlockThreads)[tid] = make_float4(wa[0], wa[1], wa[2], wa[3]);
+    __syncthreads();
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
-      rl[c] = ls[c];
-      ra[c] = a[c];
+      const int idx = min(tid + c * kBlockThreads, G * D - 1);
+      const int qd = idx / 4, col = idx % 4;
+      float M = kNegBig, ls = 0.0f, a = 0.0f;
+#pragma unroll
+      for (int u = 0; u < S; ++u) {
+        const int e = u * Q + qd;
+        const float mi = s_pool[2 * e];
+        const float mn = fmaxf(M, mi);
+        const float c_old = fast_exp2(M - mn);
+        const float c_new = fast_exp2(mi - mn);
+        ls = ls * c_old + s_pool[2 * e + 1] * c_new;
+        a = a * c_old + s_pool[2 * kBlockThreads + 4 * e + col] * c_new;
+        M = mn;
+      }
+      rl[c] = ls;
+      ra[c] = a;
     }
-  };
-  if constexpr (CPT == 1) {
-    if (n_active > 8) merge_all(std::integral_constant<int, 16>{});
-    else merge_all(std::integral_constant<int, 8>{});
-  } else {
-    merge_all(std::integral_constant<int, (CPT >= 4 ? 4 : 8)>{});
   }
   write_out(rl, ra);
   if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

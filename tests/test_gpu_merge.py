@@ -152,3 +152,36 @@ def test_q_out_partial_overlap_rejected(dev):
         assert "overlap" in str(ei.value)
     torch.cuda.synchronize()
     assert pos.cpu().tolist() == [100, 200]
+
+
+@pytest.mark.parametrize("D", [16, 32, 64, 128])
+@pytest.mark.parametrize("G", [1, 2, 4, 8])
+def test_merge_paths_every_group_shape(dev, D, G):
+    """Split counts from a few to a few hundred for every (G, D): up to 8 splits the last arriver reads one
+    (head, d) cell per thread and round (two rounds when a thread holds four cells, G * D = 1024); above 8 it
+    reads 16-byte pieces of the partials, 256 * 4 / (G * D) threads per quad of cells, combined through LDS.
+    Both match the float64 oracle, and different split counts only reorder fp32 sums."""
+    gen = torch.Generator().manual_seed(300 + 10 * G + D)
+    B, Hkv, L = 2, 2, 3200
+    scale = D ** -0.5
+    q = torch.randn((B, Hkv * G, 1, D), generator=gen).to(torch.bfloat16)
+    k = torch.randn((B, Hkv, L, D), generator=gen).to(torch.bfloat16)
+    v = torch.randn((B, Hkv, L, D), generator=gen).to(torch.bfloat16)
+    expect = ref.decode_fp64(q, k, v, scale, G)
+    view = ops.KVCacheView(k.to(dev), v.to(dev))
+    rows = 2048 // D  # rows one workgroup load covers: split sizes are multiples of it
+    outs = {}
+    for want in (rows, 128, 192, 384, 448, 640, 1600):
+        tps = -(-want // rows) * rows
+        plan = ops.decode_plan(torch.bfloat16, B, Hkv * G, Hkv, D, L, 0, tps)
+        out = ops.decode_attention(q.to(dev), view, sm_scale=scale, tokens_per_split=tps).float().cpu()
+        err = (out - expect).abs().max().item()
+        assert err < 2e-2, (plan.num_splits, err)
+        outs[plan.num_splits] = out
+    counts = sorted(outs)
+    assert counts[0] <= 8 < counts[-1], counts
+    if G * D == 1024:
+        assert any(4 < n <= 8 for n in counts), counts
+    base = outs[counts[0]]
+    for n in counts[1:]:
+        assert (outs[n] - base).abs().max() <= 2.0 ** -7 * base.abs().max(), n
