@@ -18,7 +18,7 @@ import torch  # noqa: F401  (must precede the library load, see above)
 LIB_NAME = "libaicas_decode.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 DTYPE_BF16 = 0
 DTYPE_FP16 = 1
@@ -39,6 +39,7 @@ STATUS_NONFINITE_ROW = 16
 # Entry points declared in include/aicas_decode.h, in declaration order.
 EXPORTED_SYMBOLS = (
     "aicas_kv_append",
+    "aicas_kv_gather",
     "aicas_decode_plan",
     "aicas_decode_attention",
     "aicas_decode_attention_append",
@@ -125,6 +126,12 @@ def _bind(handle: ctypes.CDLL) -> ctypes.CDLL:
         _P, _I64, _I64, _I64,
         _P, _P, _P,
         _I32, _I32, _I32, _I32,
+        _P,
+    ]
+    handle.aicas_kv_gather.restype = ctypes.c_int
+    handle.aicas_kv_gather.argtypes = [
+        ctypes.POINTER(KVCacheDesc), _P, _I32, _I32, _I32, _I32,
+        _P, _P, _I64, _I64, _I64, _I32, _P,
         _P,
     ]
     handle.aicas_decode_plan.restype = ctypes.c_int

@@ -111,15 +111,15 @@ def text_triton_attention(
         )
 
     meta = kv_descriptor(key)
-    # A ragged, paged or fp8 aicas cache defines visibility through its own per-sequence lengths and can only be
-    # read by the decode kernel, which has no per-token mask. HF hands an attention function a mask only when
-    # some position is padding (flash_attention_mask returns None for an all-ones mask), so a mask here means
-    # the kernel would attend to pad tokens: refused rather than silently ignored. Dense caches take the SDPA
-    # route with the mask, as the reference does (backends.py:235-260).
-    if attention_mask is not None and meta is not None and not meta.dense:
+    # The decode kernel has no per-token mask. HF hands an attention function a mask only when some position is
+    # padding (flash_attention_mask returns None for an all-ones mask), so a masked call takes the SDPA route
+    # with the mask, as the reference does (backends.py:235-260): dense caches as they are, paged or fp8 caches
+    # through aicas_kv_gather. A ragged aicas cache defines visibility through its own per-sequence lengths,
+    # which a padding mask over a common length cannot describe: refused rather than silently ignored.
+    if attention_mask is not None and meta is not None and not meta.dense and meta.min_seq_len != meta.max_seq_len:
         raise ValueError(
-            "a padding mask reached the decode path of a paged, fp8 or ragged aicas cache, which attends to every "
-            "cached token of a sequence: use a dense 16-bit AicasDecodeCache (or DynamicCache) for padded batches"
+            "a padding mask reached an aicas cache whose sequences have different lengths: use a cache whose "
+            "sequences advance together (HF's left padding) or no mask"
         )
     can_use_decode = (
         attention_mask is None

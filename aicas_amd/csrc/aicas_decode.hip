@@ -13,6 +13,7 @@
 #include "block_pool.hpp"
 #include "decode_attn.hpp"
 #include "kv_append.hpp"
+#include "kv_gather.hpp"
 
 // Decode launchers, one translation unit per (q dtype, kv dtype) pair (decode_<q>_<kv>.hip); they return
 // nonzero for a head_dim / group size that is not instantiated.
@@ -161,6 +162,20 @@ int launch_append_d(const aicas::AppendParams& p, int32_t batch, int32_t head_di
                        dim3(aicas::kBlockThreads), 0, s, p.positions, p.seq_lens_out, p.n_new, batch);
   }
   return check_launch("aicas_kv_append");
+}
+
+template <int KV, int OUT>
+int launch_gather_d(const aicas::GatherParams& p, int32_t batch, int32_t head_dim, hipStream_t s) {
+  const int64_t blocks = ceil_div(p.out_len, aicas::gather_rows_per_workgroup(head_dim));
+  const dim3 grid(static_cast<uint32_t>(blocks), p.num_kv_heads, batch), block(aicas::kBlockThreads);
+  switch (head_dim) {
+    case 16: hipLaunchKernelGGL((aicas::kv_gather_kernel<KV, OUT, 16>), grid, block, 0, s, p); break;
+    case 32: hipLaunchKernelGGL((aicas::kv_gather_kernel<KV, OUT, 32>), grid, block, 0, s, p); break;
+    case 64: hipLaunchKernelGGL((aicas::kv_gather_kernel<KV, OUT, 64>), grid, block, 0, s, p); break;
+    case 128: hipLaunchKernelGGL((aicas::kv_gather_kernel<KV, OUT, 128>), grid, block, 0, s, p); break;
+    default: return fail(AICAS_ERR_UNSUPPORTED, "head_dim %d not supported", head_dim);
+  }
+  return check_launch("aicas_kv_gather");
 }
 
 template <bool APPEND>
@@ -533,6 +548,60 @@ int aicas_kv_append(const aicas_kv_cache_t* cache, int32_t src_dtype, const void
   }
   if (cache->kv_dtype == kFP8E4M3) return launch_append_d<kFP16, kFP8E4M3>(p, batch, head_dim, stream);
   return launch_append_d<kFP16, kFP16>(p, batch, head_dim, stream);
+}
+
+int aicas_kv_gather(const aicas_kv_cache_t* cache, const int32_t* seq_lens, int32_t batch, int32_t num_kv_heads,
+                    int32_t head_dim, int32_t out_dtype, void* k_out, void* v_out, int64_t out_stride_b,
+                    int64_t out_stride_h, int64_t out_stride_t, int32_t out_len, int32_t* status,
+                    hipStream_t stream) {
+  if (batch <= 0 || num_kv_heads <= 0 || out_len < 0)
+    return fail(AICAS_ERR_INVALID, "batch and num_kv_heads must be positive and out_len non-negative");
+  if (batch > 65535 || num_kv_heads > 65535)
+    return fail(AICAS_ERR_UNSUPPORTED, "batch %d / num_kv_heads %d exceed 65535", batch, num_kv_heads);
+  if (!valid_head_dim(head_dim)) return fail(AICAS_ERR_UNSUPPORTED, "head_dim %d not supported", head_dim);
+  if (out_dtype != AICAS_DTYPE_BF16 && out_dtype != AICAS_DTYPE_FP16)
+    return fail(AICAS_ERR_UNSUPPORTED, "the gathered rows must be bf16 or fp16");
+  if (!seq_lens || !k_out || !v_out) return fail(AICAS_ERR_INVALID, "seq_lens, k_out and v_out must be non-NULL");
+  if (!aligned16(k_out) || !aligned16(v_out)) return fail(AICAS_ERR_INVALID, "k_out and v_out must be 16-byte aligned");
+  if ((out_stride_b % 8) || (out_stride_h % 8) || (out_stride_t % 8) || out_stride_b < 0 || out_stride_h < 0 ||
+      out_stride_t < head_dim)
+    return fail(AICAS_ERR_INVALID, "output strides must be non-negative multiples of 8 elements, token stride >= head_dim");
+  aicas::GatherParams p{};
+  int rc = make_layout(cache, batch, num_kv_heads, head_dim, p.cache);
+  if (rc) return rc;
+  if (cache->kv_dtype != AICAS_DTYPE_FP8_E4M3 && cache->kv_dtype != out_dtype)
+    return fail(AICAS_ERR_UNSUPPORTED, "a 16-bit cache is gathered into its own dtype");
+  if (out_len == 0) return ok();
+  // the outputs may overlap neither each other nor the cache they are read from
+  auto span = [](const void* ptr, int64_t last_elem, int eb) -> Extent {
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(ptr);
+    return {lo, lo + static_cast<uintptr_t>(last_elem) * eb};
+  };
+  const int64_t out_last = (batch - 1) * out_stride_b + (num_kv_heads - 1) * out_stride_h +
+                           int64_t{out_len - 1} * out_stride_t + head_dim;
+  const int64_t cache_last = (p.cache.num_blocks - 1) * cache->stride_blk + (num_kv_heads - 1) * cache->stride_h +
+                             int64_t{cache->page_size - 1} * cache->stride_t + head_dim;
+  const int eb = elem_bytes(cache->kv_dtype);
+  const Extent ko = span(k_out, out_last, 2), vo = span(v_out, out_last, 2);
+  const Extent kc = span(cache->k, cache_last, eb), vc = span(cache->v, cache_last, eb);
+  if (overlaps(ko, vo) || overlaps(ko, kc) || overlaps(ko, vc) || overlaps(vo, kc) || overlaps(vo, vc))
+    return fail(AICAS_ERR_INVALID, "k_out / v_out overlap each other or the cache");
+  p.seq_lens = seq_lens;
+  p.k_out = k_out;
+  p.v_out = v_out;
+  p.out_stride_b = out_stride_b;
+  p.out_stride_h = out_stride_h;
+  p.out_stride_t = out_stride_t;
+  p.out_len = out_len;
+  p.num_kv_heads = num_kv_heads;
+  p.status = status;
+  using namespace aicas;
+  if (cache->kv_dtype == kFP8E4M3) {
+    return out_dtype == kBF16 ? launch_gather_d<kFP8E4M3, kBF16>(p, batch, head_dim, stream)
+                              : launch_gather_d<kFP8E4M3, kFP16>(p, batch, head_dim, stream);
+  }
+  return out_dtype == kBF16 ? launch_gather_d<kBF16, kBF16>(p, batch, head_dim, stream)
+                            : launch_gather_d<kFP16, kFP16>(p, batch, head_dim, stream);
 }
 
 int aicas_decode_plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,

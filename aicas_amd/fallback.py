@@ -44,6 +44,15 @@ def _padding_mask_4d(attention_mask: torch.Tensor, q_len: int, kv_len: int, caus
                      attention_mask=attention_mask.bool(), allow_is_causal_skip=False, device=attention_mask.device)
 
 
+def _causal_continuation_mask(batch: int, q_len: int, kv_len: int, device: torch.device) -> torch.Tensor:
+    """Boolean [B, 1, q, kv] visibility of q_len queries that follow kv_len - q_len cached tokens: query i sits
+    at position kv_len - q_len + i and sees keys j <= that position (the alignment of HF's own causal mask for a
+    cache, transformers/masking_utils.py causal_mask_function with q_offset = kv_len - q_len)."""
+    i = torch.arange(q_len, device=device)[:, None]
+    j = torch.arange(kv_len, device=device)[None, :]
+    return (j <= i + (kv_len - q_len))[None, None].expand(batch, 1, q_len, kv_len)
+
+
 def sdpa_fallback(
     module: torch.nn.Module,
     query: torch.Tensor,
@@ -55,15 +64,26 @@ def sdpa_fallback(
     is_causal: bool | None = None,
     **kwargs,
 ) -> tuple[torch.Tensor, None]:
-    if getattr(key, "_aicas_kv", None) is not None and not key._aicas_kv.dense:
-        raise RuntimeError(
-            "this KV cache is paged or fp8 and can only be read by the aicas decode kernel; "
-            "SDPA cannot consume it (decode with attention_mask=None, q_len=1)"
-        )
+    meta = getattr(key, "_aicas_kv", None)
+    if meta is not None and not meta.dense:
+        # a paged or fp8 aicas cache: its rows as dense 16-bit K/V (fp8 dequantised), every sequence being
+        # max_seq_len long; a ragged one has no single causal offset for the new queries and is refused
+        if meta.min_seq_len != meta.max_seq_len:
+            raise RuntimeError(
+                "this aicas KV cache holds sequences of different lengths; only the decode kernel reads it "
+                "(attention_mask=None, q_len=1)"
+            )
+        from . import ops
+
+        key, value = ops.kv_gather(meta.cache, meta.seq_lens, meta.max_seq_len, dtype=query.dtype)
+    causal = bool(is_causal if is_causal is not None else getattr(module, "is_causal", True))
+    q_len, kv_len = query.shape[2], key.shape[2]
     sdpa_attention_forward = _load_sdpa_attention_forward()
-    if sdpa_attention_forward is not None and attention_mask is not None and attention_mask.dim() == 2:
-        causal = is_causal if is_causal is not None else getattr(module, "is_causal", True)
-        attention_mask = _padding_mask_4d(attention_mask, query.shape[2], key.shape[2], bool(causal))
+    if attention_mask is None and causal and 1 < q_len < kv_len:
+        # queries continuing a cached prefix: SDPA's is_causal would align them with the first keys
+        attention_mask = _causal_continuation_mask(query.shape[0], q_len, kv_len, query.device)
+    elif sdpa_attention_forward is not None and attention_mask is not None and attention_mask.dim() == 2:
+        attention_mask = _padding_mask_4d(attention_mask, q_len, kv_len, causal)
     if sdpa_attention_forward is not None:
         return sdpa_attention_forward(
             module, query, key, value, attention_mask, dropout=dropout, scaling=scaling, is_causal=is_causal,

@@ -191,6 +191,50 @@ def kv_append(
     )
 
 
+def kv_gather(
+    cache: KVCacheView,
+    seq_lens: torch.Tensor,
+    out_len: int,
+    dtype: torch.dtype | None = None,
+    out: tuple[torch.Tensor, torch.Tensor] | None = None,
+    status: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """The first ``seq_lens[b]`` tokens of every sequence as dense ``[B, Hkv, out_len, D]`` K and V (rows past
+    a sequence's length zero): a 16-bit cache copied as it is, an fp8 cache dequantised (code * scale in fp32,
+    rounded once to ``dtype``, bf16 by default). What a prefill's attention reads from a paged or fp8 cache
+    (new KV cache/evaluation_wrapper.py:198-245, ``_gather_paged_kv_cache``)."""
+    if seq_lens.dtype != torch.int32 or not seq_lens.is_contiguous() or seq_lens.dim() != 1:
+        raise AicasError(_lib.ERR_INVALID, "seq_lens must be a contiguous 1-D int32 tensor")
+    B = seq_lens.numel()
+    if cache.block_table is not None and cache.block_table.shape[0] < B:
+        raise AicasError(_lib.ERR_INVALID, "the block table has fewer rows than seq_lens")
+    if cache.block_table is None and cache.k.shape[0] < B:
+        raise AicasError(_lib.ERR_INVALID, "the cache holds fewer sequences than seq_lens")
+    if dtype is None:
+        dtype = torch.bfloat16 if cache.is_fp8 else cache.k.dtype
+    shape = (B, cache.num_kv_heads, int(out_len), cache.head_dim)
+    if out is None:
+        k_out = torch.empty(shape, dtype=dtype, device=cache.device)
+        v_out = torch.empty(shape, dtype=dtype, device=cache.device)
+    else:
+        k_out, v_out = out
+        for t, name in ((k_out, "k_out"), (v_out, "v_out")):
+            if tuple(t.shape) != shape or t.dtype != dtype or t.stride(3) != 1:
+                raise AicasError(_lib.ERR_INVALID, f"{name} must be {shape} {dtype} with unit head_dim stride")
+        if k_out.stride() != v_out.stride():
+            raise AicasError(_lib.ERR_INVALID, "k_out and v_out must share strides")
+    _require_gpu(cache.k, seq_lens, k_out, v_out, status)
+    desc = cache.desc()
+    check(
+        _lib.lib().aicas_kv_gather(
+            ctypes.byref(desc), seq_lens.data_ptr(), B, cache.num_kv_heads, cache.head_dim, dtype_code(dtype),
+            k_out.data_ptr(), v_out.data_ptr(), k_out.stride(0), k_out.stride(1), k_out.stride(2), int(out_len),
+            _ptr(status), _stream(cache.device),
+        )
+    )
+    return k_out, v_out
+
+
 class BlockPool:
     """Free block ids of a paged cache's pool, kept on the device (``aicas_block_pool_t``): ``alloc`` gives the
     pages an append is about to touch a block, ``free`` takes a finished sequence's blocks back — both kernels

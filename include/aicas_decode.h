@@ -19,6 +19,9 @@
  *                              triton_qwen3vl/gqa_decode_attention.py:268-327 and :46-141;
  *                              decode_q1_gqa_forward, dujunbaoV1/native_cuda_ops/decode_q1_gqa.cpp:73-95;
  *                              _paged_kv_attention, new KV cache/evaluation_wrapper.py:248-265.
+ *   aicas_kv_gather         <- _gather_paged_kv_cache, new KV cache/evaluation_wrapper.py:198-245 (the paged,
+ *                              quantised cache dequantised into dense rows for a prefill's attention, called at
+ *                              :428-453).
  *   aicas_decode_plan       <- the launch-configuration choice, triton_qwen3vl/gqa_decode_attention.py:287-292.
  *   aicas_last_error        <- the ValueError / TORCH_CHECK messages, gqa_decode_attention.py:282 and
  *                              decode_q1_gqa.cpp:65-92.
@@ -35,7 +38,7 @@
 extern "C" {
 #endif
 
-#define AICAS_ABI_VERSION 6
+#define AICAS_ABI_VERSION 7
 
 /* Element types. */
 #define AICAS_DTYPE_BF16 0
@@ -102,6 +105,22 @@ int aicas_kv_append(const aicas_kv_cache_t* cache, int32_t src_dtype, const void
                     int64_t k_stride_h, int64_t k_stride_t, const void* v_src, int64_t v_stride_b,
                     int64_t v_stride_h, int64_t v_stride_t, const int32_t* positions, int32_t* seq_lens_out,
                     int32_t* status, int32_t batch, int32_t num_kv_heads, int32_t head_dim, int32_t n_new,
+                    hipStream_t stream);
+
+/*
+ * The first seq_lens[b] tokens of every (batch row b, kv head h) of the cache as dense rows: k_out[b, h, t, :] and
+ * v_out[b, h, t, :] for t < out_len (element strides out_stride_b / _h / _t, head_dim stride 1; out_dtype bf16 or
+ * fp16), rows at or past seq_lens[b] zero. A 16-bit cache is copied bit for bit (out_dtype must be its dtype); an
+ * fp8 cache comes out as code * scale computed in fp32 and rounded to out_dtype once (nearest even; a poisoned
+ * row, scale NaN, comes out NaN). Lengths beyond the cache are clamped (AICAS_STATUS_LEN_CLAMPED), invalid block
+ * ids give zero rows (AICAS_STATUS_BLOCK_OUT_OF_RANGE); status may be NULL. The outputs may overlap neither each
+ * other nor the cache. What a prefill's attention reads from a paged or fp8 cache: the rows the decode kernel
+ * attends to, in the layout other attention backends take.
+ * Replaces: _gather_paged_kv_cache, new KV cache/evaluation_wrapper.py:198-245.
+ */
+int aicas_kv_gather(const aicas_kv_cache_t* cache, const int32_t* seq_lens, int32_t batch, int32_t num_kv_heads,
+                    int32_t head_dim, int32_t out_dtype, void* k_out, void* v_out, int64_t out_stride_b,
+                    int64_t out_stride_h, int64_t out_stride_t, int32_t out_len, int32_t* status,
                     hipStream_t stream);
 
 /*

@@ -233,10 +233,11 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     assert patch.hip_decode_available() is False
 
 
-def test_padding_mask_on_kernel_only_cache_is_refused(monkeypatch):
-    """A padding mask cannot be applied to a paged / fp8 / ragged aicas cache (the kernel attends to every cached
-    token of a sequence): the attention function raises instead of dropping the mask. A dense cache with a mask
-    takes the SDPA route, as the reference's does."""
+def test_padding_mask_routes_to_sdpa_or_is_refused(monkeypatch):
+    """A padding mask never reaches the decode kernel (it attends to every cached token of a sequence). On a cache
+    whose sequences advance together — dense, or paged / fp8 read through aicas_kv_gather — the call takes the
+    SDPA route with the mask, as the reference's does; on a ragged aicas cache the attention function raises
+    instead of dropping the mask."""
     from aicas_amd.gqa_decode_attention import AicasKV
 
     monkeypatch.setattr(backends, "can_use_gqa_decode_attention", lambda *args, **kwargs: True)
@@ -245,7 +246,7 @@ def test_padding_mask_on_kernel_only_cache_is_refused(monkeypatch):
     module = DummyAttentionModule(num_key_value_groups=2)
     q, k, v = torch.randn(2, 4, 1, 8), torch.randn(2, 2, 6, 8), torch.randn(2, 2, 6, 8)
     mask = torch.tensor([[0, 1, 1, 1, 1, 1], [1, 1, 1, 1, 1, 1]], dtype=torch.bool)
-    k._aicas_kv = AicasKV(cache=None, seq_lens=None, max_seq_len=6, batch=2, dense=False)
+    k._aicas_kv = AicasKV(cache=None, seq_lens=None, max_seq_len=6, min_seq_len=4, batch=2, dense=False)
     with pytest.raises(ValueError, match="padding mask"):
         text_triton_attention(module, q, k, v, attention_mask=mask)
     recorded = {}
@@ -255,9 +256,37 @@ def test_padding_mask_on_kernel_only_cache_is_refused(monkeypatch):
         return torch.zeros(2, 1, 4, 8), None
 
     monkeypatch.setattr(backends, "sdpa_fallback", fake_sdpa)
-    k._aicas_kv = AicasKV(cache=None, seq_lens=None, max_seq_len=6, batch=2, dense=True)
-    text_triton_attention(module, q, k, v, attention_mask=mask)
-    assert recorded["mask"] is mask
+    for dense in (True, False):  # dense 16-bit; paged or fp8 with every sequence 6 tokens long
+        recorded.clear()
+        k._aicas_kv = AicasKV(cache=None, seq_lens=None, max_seq_len=6, min_seq_len=6, batch=2, dense=dense)
+        text_triton_attention(module, q, k, v, attention_mask=mask)
+        assert recorded["mask"] is mask
+
+
+def test_continuing_prefill_mask_is_bottom_right_causal():
+    """Queries that follow cached tokens (q_len > 1, no mask) see every cached key and the new ones up to their
+    own position — HF's causal alignment for a cache — not SDPA's top-left is_causal."""
+    from aicas_amd.fallback import _causal_continuation_mask
+
+    m = _causal_continuation_mask(2, 3, 7, torch.device("cpu"))
+    assert m.shape == (2, 1, 3, 7)
+    expect = torch.tensor([[1, 1, 1, 1, 1, 0, 0], [1, 1, 1, 1, 1, 1, 0], [1, 1, 1, 1, 1, 1, 1]], dtype=torch.bool)
+    assert torch.equal(m[0, 0], expect) and torch.equal(m[1, 0], expect)
+    # a fresh prompt (q_len == kv_len) is the plain lower triangle
+    assert torch.equal(_causal_continuation_mask(1, 4, 4, torch.device("cpu"))[0, 0],
+                       torch.ones(4, 4, dtype=torch.bool).tril())
+
+
+def test_continuing_prefill_through_sdpa_fallback_matches_full_attention():
+    """A prompt split in two prefills (the second continuing the first through a dense cache) gives the rows a
+    single prefill over the whole prompt gives, on the CPU SDPA route."""
+    torch.manual_seed(3)
+    module = DummyAttentionModule(num_key_value_groups=2)
+    q = torch.randn(1, 4, 7, 8)
+    k, v = torch.randn(1, 2, 7, 8), torch.randn(1, 2, 7, 8)
+    whole, _ = backends.sdpa_fallback(module, q, k, v, None, scaling=8 ** -0.5)
+    tail, _ = backends.sdpa_fallback(module, q[:, :, 4:], k, v, None, scaling=8 ** -0.5)
+    torch.testing.assert_close(tail, whole[:, 4:], rtol=1e-5, atol=1e-6)
 
 
 def test_cache_layer_refuses_beam_reordering():
