@@ -181,6 +181,13 @@ __device__ __forceinline__ uint4 load_stream16(const void* p) {
   return make_uint4(w.x, w.y, w.z, w.w);
 }
 
+// 16 bytes stored non-temporal: a stream written once, kept from allocating in L2 and the memory-side cache.
+__device__ __forceinline__ void store_stream16(void* p, uint4 v) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, static_cast<u32x4*>(p));
+}
+
 // Where a token's K/V row lives. Contiguous caches are the one-block-per-sequence case:
 // block id = batch index, page_size = capacity, and the token stride may be any multiple of 16 bytes.
 struct KVLayout {

@@ -52,43 +52,56 @@ __global__ __launch_bounds__(kBlockThreads) void kv_gather_kernel(GatherParams p
   }
   L = max(0, min(L, p.out_len));
 
-  // Source rows of every pass, loaded before any conversion.
-  uint4 kw[kGatherPasses], vw[kGatherPasses];  // 16-bit: 8 elements; fp8: 8 codes in .x, .y
-  float ks[kGatherPasses], vs[kGatherPasses];
+  // Source rows of every pass, loaded before any conversion. Every load is issued unconditionally (a pass past
+  // the length, or behind an invalid block id, reads an in-bounds row and is masked afterwards), so the loads
+  // are in flight together: the block ids of all passes first, then the rows.
+  int64_t blk[kGatherPasses];
+  int tin[kGatherPasses];
   bool ok[kGatherPasses];
+  if (p.cache.block_table) {
+    const int32_t* const row_ids = p.cache.block_table + static_cast<int64_t>(b) * p.cache.block_table_stride;
 #pragma unroll
-  for (int k = 0; k < kGatherPasses; ++k) {
-    const int t = t0 + k * ROWS_PER_PASS;
-    ok[k] = false;
-    kw[k] = vw[k] = make_uint4(0u, 0u, 0u, 0u);
-    ks[k] = vs[k] = 0.0f;
-    if (t < L) {
-      int64_t blk = b;
-      int tin = t;
-      if (p.cache.block_table) {
-        blk = p.cache.block_table[static_cast<int64_t>(b) * p.cache.block_table_stride + t / p.cache.page_size];
-        tin = t % p.cache.page_size;
-      }
-      if (blk >= 0 && blk < p.cache.num_blocks) {
-        ok[k] = true;
-        const int64_t row = blk * p.cache.stride_blk + h * p.cache.stride_h + static_cast<int64_t>(tin) * p.cache.stride_t;
-        if constexpr (FP8) {
-          const uint2 kc = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(p.cache.k) + row + lane * VEC);
-          const uint2 vc = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(p.cache.v) + row + lane * VEC);
-          kw[k] = make_uint4(kc.x, kc.y, 0u, 0u);
-          vw[k] = make_uint4(vc.x, vc.y, 0u, 0u);
-          const int64_t srow = blk * p.cache.scale_stride_blk + h * p.cache.scale_stride_h + tin;
-          ks[k] = p.cache.k_scale[srow];
-          vs[k] = p.cache.v_scale[srow];
-        } else {
-          kw[k] = load_stream16(static_cast<const uint16_t*>(p.cache.k) + row + lane * VEC);
-          vw[k] = load_stream16(static_cast<const uint16_t*>(p.cache.v) + row + lane * VEC);
-        }
-      } else if (p.status && lane == 0) {
-        atomicOr(p.status, kStatusBlockOutOfRange);
-      }
+    for (int k = 0; k < kGatherPasses; ++k) {
+      const int tc = min(t0 + k * ROWS_PER_PASS, max(L - 1, 0));
+      blk[k] = row_ids[tc / p.cache.page_size];
+      tin[k] = tc % p.cache.page_size;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < kGatherPasses; ++k) {
+      blk[k] = b;
+      tin[k] = min(t0 + k * ROWS_PER_PASS, max(L - 1, 0));
     }
   }
+  bool bad = false;
+#pragma unroll
+  for (int k = 0; k < kGatherPasses; ++k) {
+    const bool valid = blk[k] >= 0 && blk[k] < p.cache.num_blocks;
+    const bool live = t0 + k * ROWS_PER_PASS < L;
+    ok[k] = live && valid;
+    bad |= live && !valid;
+    if (!valid) blk[k] = 0;
+  }
+  uint4 kw[kGatherPasses], vw[kGatherPasses];  // 16-bit: 8 elements; fp8: 8 codes in .x, .y
+  float ks[kGatherPasses], vs[kGatherPasses];
+#pragma unroll
+  for (int k = 0; k < kGatherPasses; ++k) {
+    const int64_t row = blk[k] * p.cache.stride_blk + h * p.cache.stride_h + static_cast<int64_t>(tin[k]) * p.cache.stride_t;
+    if constexpr (FP8) {
+      const uint2 kc = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(p.cache.k) + row + lane * VEC);
+      const uint2 vc = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(p.cache.v) + row + lane * VEC);
+      kw[k] = make_uint4(kc.x, kc.y, 0u, 0u);
+      vw[k] = make_uint4(vc.x, vc.y, 0u, 0u);
+      const int64_t srow = blk[k] * p.cache.scale_stride_blk + h * p.cache.scale_stride_h + tin[k];
+      ks[k] = p.cache.k_scale[srow];
+      vs[k] = p.cache.v_scale[srow];
+    } else {
+      kw[k] = load_stream16(static_cast<const uint16_t*>(p.cache.k) + row + lane * VEC);
+      vw[k] = load_stream16(static_cast<const uint16_t*>(p.cache.v) + row + lane * VEC);
+    }
+  }
+
+  if (bad && p.status && lane == 0) atomicOr(p.status, kStatusBlockOutOfRange);
 
   // fp8: 8 codes (two dwords) -> 8 values code * scale, rounded to OUT_DT and packed in 4 dwords
   auto dequant = [](uint32_t w0, uint32_t w1, float scale) -> uint4 {
@@ -115,13 +128,12 @@ __global__ __launch_bounds__(kBlockThreads) void kv_gather_kernel(GatherParams p
     if (t >= p.out_len) continue;
     uint4 a = kw[k], c = vw[k];
     if constexpr (FP8) {
-      if (ok[k]) {
-        a = dequant(kw[k].x, kw[k].y, ks[k]);
-        c = dequant(vw[k].x, vw[k].y, vs[k]);
-      }
+      a = dequant(kw[k].x, kw[k].y, ks[k]);
+      c = dequant(vw[k].x, vw[k].y, vs[k]);
     }
-    *reinterpret_cast<uint4*>(ko + static_cast<int64_t>(t) * p.out_stride_t) = a;
-    *reinterpret_cast<uint4*>(vo + static_cast<int64_t>(t) * p.out_stride_t) = c;
+    if (!ok[k]) a = c = make_uint4(0u, 0u, 0u, 0u);
+    store_stream16(ko + static_cast<int64_t>(t) * p.out_stride_t, a);
+    store_stream16(vo + static_cast<int64_t>(t) * p.out_stride_t, c);
   }
 }
 

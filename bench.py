@@ -61,7 +61,8 @@ MALL_BYTES = 256 << 20
 def parse_args(argv=None):
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--config", choices=("c1", "c2", "c3", "c4", "c5", "model", "microbench", "calib"), default="c2",
+    p.add_argument("--config", choices=("c1", "c2", "c3", "c4", "c5", "model", "microbench", "calib", "gather"),
+                   default="c2",
                    help="model: the whole text-decoder step per generated token; microbench: the shape of the "
                         "reference's published decode microbenchmark (both reported separately)")
     p.add_argument("--prompt-len", type=int, default=1024, help="model: cached tokens before the timed steps")
@@ -500,6 +501,128 @@ def calib(args) -> int:
     return 0
 
 
+def gather(args) -> int:
+    """--config gather: aicas_kv_gather over the C5 cache (B=32, lengths U{256..8192}, 16-token pages over a
+    permuted block table, fp8 e4m3 codes + fp32 scales per (token, kv head)) into dense bf16 K and V
+    [32, 8, max_len, 128]: what a prefill's attention reads from that cache. Bytes per launch: the cached rows
+    read (codes and scales) plus the dense rows written (max_len per sequence, zeros past its length). Two
+    distinct caches alternate in the graph, so the 256 MB memory-side cache cannot serve the reads; µs per launch
+    = graph time / launches. The CPU baseline is the oracle's gather + dequantisation of the same cache
+    (torch on the host cores) over a bounded sample of its sequences."""
+    import torch
+
+    from aicas_amd import ops
+    from aicas_amd.workloads import HEAD_DIM as D, HKV, PAGE, WORKLOADS, generator, normal, seq_lengths
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    w = WORKLOADS["c5"]
+    gen = generator(dev, w.seed)
+    lens = seq_lengths(w, gen)
+    B, NL, reps = w.batch, 2, args.steps or 20
+    max_len = max(lens)
+    views = []
+    for _ in range(NL):
+        per_seq = [(L + PAGE - 1) // PAGE for L in lens]
+        nblocks = sum(per_seq)
+        perm = torch.randperm(nblocks, generator=gen, device=dev).to(torch.int32)
+        bt = torch.full((B, max(per_seq)), -1, dtype=torch.int32, device=dev)
+        at = 0
+        for b, n in enumerate(per_seq):
+            bt[b, :n] = perm[at : at + n]
+            at += n
+        kp = torch.zeros((nblocks, HKV, PAGE, D), dtype=ops.FP8_DTYPE, device=dev)
+        vp = torch.zeros_like(kp)
+        ksc = torch.zeros((nblocks, HKV, PAGE), dtype=torch.float32, device=dev)
+        vsc = torch.zeros_like(ksc)
+        view = ops.KVCacheView(kp, vp, ksc, vsc, bt)
+        for b, L in enumerate(lens):
+            rows_k = normal((1, HKV, L, D), gen, dev, outlier_frac=w.outlier_frac, outlier_value=w.outlier_value)
+            rows_v = normal((1, HKV, L, D), gen, dev, outlier_frac=w.outlier_frac, outlier_value=w.outlier_value)
+            ops.kv_append(ops.KVCacheView(kp, vp, ksc, vsc, bt[b : b + 1]), rows_k, rows_v,
+                          torch.zeros(1, dtype=torch.int32, device=dev))
+        views.append(view)
+    seq_lens = torch.tensor(lens, dtype=torch.int32, device=dev)
+    k_out = torch.empty((B, HKV, max_len, D), dtype=torch.bfloat16, device=dev)
+    v_out = torch.empty_like(k_out)
+    read_bytes = 2 * sum(lens) * HKV * (D + 4)
+    write_bytes = 2 * B * HKV * max_len * D * 2
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        for v in views:
+            ops.kv_gather(v, seq_lens, max_len, out=(k_out, v_out))
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for v in views:
+                ops.kv_gather(v, seq_lens, max_len, out=(k_out, v_out))
+        for _ in range(3):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * NL)
+    gbps = (read_bytes + write_bytes) / (us * 1e-6) / 1e9
+
+    # parity of the last launch (the second cache) against the oracle, on a few sequences
+    from oracle import reference_path as ref
+
+    view = views[-1]
+    check = [0, 1, B - 1]
+    kc, ks_c, bt_c = view.k.cpu(), view.k_scale.cpu(), view.block_table.cpu()
+    max_err = 0
+    for b in check:
+        codes = ref.paged_gather(kc, bt_c[b : b + 1], [lens[b]])[0]
+        scale = ref.paged_gather(ks_c[..., None], bt_c[b : b + 1], [lens[b]])[0][..., 0]
+        want = ref.fp8_dequantize_rows(codes, scale).to(torch.bfloat16)
+        got = k_out[b, :, : lens[b]].cpu()
+        max_err = max(max_err, int((got.view(torch.int16) != want.view(torch.int16)).sum()))
+
+    cpu = None
+    if args.cpu_baseline_seconds > 0:
+        threads, core_info = host_cores()
+        torch.set_num_threads(threads)
+        vc, vs_c = view.v.cpu(), view.v_scale.cpu()
+        t_s, done, tokens = time.perf_counter(), 0, 0
+        for b in range(B):
+            for pool, sc in ((kc, ks_c), (vc, vs_c)):
+                codes = ref.paged_gather(pool, bt_c[b : b + 1], [lens[b]])[0]
+                scale = ref.paged_gather(sc[..., None], bt_c[b : b + 1], [lens[b]])[0][..., 0]
+                dense = torch.zeros((HKV, max_len, D), dtype=torch.bfloat16)
+                dense[:, : lens[b]] = ref.fp8_dequantize_rows(codes, scale).to(torch.bfloat16)
+            done += 1
+            tokens += lens[b]
+            if time.perf_counter() - t_s > args.cpu_baseline_seconds:
+                break
+        cpu_s = time.perf_counter() - t_s
+        cpu_us = cpu_s / done * B * 1e6
+        cpu = {"value": round(cpu_us, 1), "unit": "us/launch", "cores": threads, **core_info, "kind": "port",
+               "sample": f"the oracle's paged gather + fp8 dequantisation (torch {torch.__version__}, host) of "
+                         f"{done} of the {B} sequences ({tokens} tokens), scaled to all {B}"}
+    result = {
+        "metric": "us per aicas_kv_gather launch & achieved HBM GB/s (% of 8 TB/s): the C5 paged fp8 cache as "
+                  "dense bf16 rows (reported beside the headline, not the headline)",
+        "value": round(us, 2), "unit": "us/launch", "n_gpus": 1, "steps": reps, "warmup": 3,
+        "ms_per_step": round(us / 1e3, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp8->bf16", "data": "synthetic (seeded N(0,1), 1% outliers +-8)",
+        "config": {"workload": f"kv gather: B={B}, 8 kv heads, head_dim 128, lengths U{{256..8192}} (max {max_len}), "
+                               "16-token pages, fp8 e4m3 + fp32 scales -> bf16", "batch": B, "max_len": max_len,
+                   "cache_instances": NL},
+        "roofline": {"bound": "hbm", "kernel": "kv_gather_kernel<fp8,bf16,D=128>", "achieved": round(gbps, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "bytes_per_launch": read_bytes + write_bytes, "read_bytes": read_bytes,
+                     "write_bytes": write_bytes, "avg_launch_us": round(us, 3)},
+        "cpu_baseline": cpu,
+        "parity_mismatched_elements": max_err,
+    }
+    print(json.dumps(result), flush=True)
+    return 0 if max_err == 0 else 1
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.config == "model" and args.gpus == 1:
@@ -508,6 +631,8 @@ def main(argv=None) -> int:
         return microbench(args)
     if args.config == "calib" and args.gpus == 1:
         return calib(args)
+    if args.config == "gather" and args.gpus == 1:
+        return gather(args)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: each GPU serves its own "
               "sequences (or kv heads), so the step does not shard across GPUs here.", file=sys.stderr)
