@@ -1,5 +1,10 @@
-// Bandwidth calibration kernels for bench.py --config calib (libaicas_calib.so; not part of the decode ABI).
+// Calibration and self-check kernels (libaicas_calib.so; not part of the decode ABI).
 //
+// aicas_calib_fp8_encoder_check: the fp8 encoding the kernels use (e4m3x4, gfx950's v_cvt_pk_fp8_f32) against
+// the encoder written out from the format (f32_to_e4m3) on every float with |x| <= 448; a GPU test requires
+// zero mismatches.
+//
+// Bandwidth calibration for bench.py --config calib:
 // They read exactly the bytes one decode launch of a contiguous bf16 cache reads (K and V rows of B sequences x
 // Hkv heads x L tokens, head_dim 128) and compute nothing but an xor of the words, so that their time is the
 // streaming ceiling the attention launch is compared with:
@@ -70,6 +75,32 @@ __global__ __launch_bounds__(aicas::kBlockThreads) void flat_read_kernel(const u
 
 __global__ void empty_kernel() {}
 
+// Thread gid of a launch covers the 16 bit patterns (slice << 28) | (16 * gid + i); 2^24 threads cover a slice.
+__global__ __launch_bounds__(aicas::kBlockThreads) void fp8_encoder_check_kernel(uint32_t slice,
+                                                                                unsigned long long* mismatches,
+                                                                                uint32_t* first) {
+  const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
+  unsigned long long bad = 0;
+#pragma unroll
+  for (int i = 0; i < 16; i += 4) {
+    float x[4];
+    uint32_t sw = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t u = (slice << 28) | (16u * gid + static_cast<uint32_t>(i + j));
+      x[j] = __uint_as_float(u);
+      if (!(fabsf(x[j]) <= 448.0f)) x[j] = 0.0f;  // outside the domain: compare zeros
+      sw |= aicas::f32_to_e4m3(x[j]) << (8 * j);
+    }
+    const uint32_t hw = aicas::e4m3x4(x[0], x[1], x[2], x[3]);
+    if (hw != sw) {
+      ++bad;
+      atomicCAS(first, 0xffffffffu, (slice << 28) | (16u * gid + static_cast<uint32_t>(i)));
+    }
+  }
+  if (bad) atomicAdd(mismatches, bad);
+}
+
 }  // namespace
 
 extern "C" {
@@ -91,6 +122,21 @@ int aicas_calib_flat_read(const void* k, const void* v, int64_t n_bytes, int32_t
   hipLaunchKernelGGL(flat_read_kernel, dim3(blocks), dim3(aicas::kBlockThreads), 0, stream,
                      static_cast<const uint4*>(k), static_cast<const uint4*>(v), n_bytes / 16, sink);
   return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+// Every float with |x| <= 448 through both encoders, 4 at a time; *mismatches (zeroed here) counts the groups of
+// 4 whose codes differ, *first_pattern (set to 0xffffffff here) the first bit pattern of one of them.
+// Synchronous: returns after the 16 launches have finished.
+int aicas_calib_fp8_encoder_check(unsigned long long* mismatches, uint32_t* first_pattern, hipStream_t stream) {
+  if (!mismatches || !first_pattern) return 1;
+  if (hipMemsetAsync(mismatches, 0, sizeof(unsigned long long), stream) != hipSuccess) return 2;
+  if (hipMemsetAsync(first_pattern, 0xff, sizeof(uint32_t), stream) != hipSuccess) return 2;
+  for (uint32_t slice = 0; slice < 16; ++slice) {
+    hipLaunchKernelGGL(fp8_encoder_check_kernel, dim3((1u << 24) / aicas::kBlockThreads), dim3(aicas::kBlockThreads),
+                       0, stream, slice, mismatches, first_pattern);
+    if (hipGetLastError() != hipSuccess) return 2;
+  }
+  return hipStreamSynchronize(stream) == hipSuccess ? 0 : 2;
 }
 
 int aicas_calib_empty(hipStream_t stream) {

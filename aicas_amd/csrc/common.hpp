@@ -107,8 +107,9 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
 }
 
 // OCP FP8 E4M3 ("e4m3fn": bias 7, no infinities, S.1111.111 is NaN, max finite 448).
-// Encoder: round to nearest even; |x| is expected to be <= 448 already (callers clamp), and
-// NaN maps to 0x7f with the sign kept.
+// Encoder written out from the format: round to nearest even; |x| is expected to be <= 448 already (callers
+// clamp), and NaN maps to 0x7f with the sign kept. The kernels encode with e4m3x4 (the hardware conversion);
+// this is what aicas_calib_fp8_encoder_check holds it to.
 __device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
   const uint32_t u = __float_as_uint(x);
   const uint32_t sign = (u >> 24) & 0x80u;
@@ -126,6 +127,14 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
   const uint32_t rem = man & 0xfffffu;
   if (rem > 0x80000u || (rem == 0x80000u && (m3 & 1u))) m3 += 1u;
   return sign | ((exp << 3) + m3);  // a mantissa carry rolls into the exponent field
+}
+
+// Four floats with |x| <= 448 -> their OCP e4m3 codes (round to nearest even), byte i the code of the i-th: two
+// gfx950 v_cvt_pk_fp8_f32. On that domain (both zeros and the subnormals included) it gives f32_to_e4m3's codes
+// for every float; libaicas_calib.so's aicas_calib_fp8_encoder_check compares the two over all of them.
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false));
+  return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, static_cast<int>(lo), true));
 }
 
 // Cross-lane reductions inside aligned groups of N lanes (N <= 16, one DPP row), result in every lane.
@@ -179,6 +188,13 @@ __device__ __forceinline__ uint4 load_stream16(const void* p) {
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   const u32x4 w = __builtin_nontemporal_load(static_cast<const u32x4*>(p));
   return make_uint4(w.x, w.y, w.z, w.w);
+}
+
+// vmcnt(0): wait until this wave's vector memory operations (loads and stores) have completed.
+__device__ __forceinline__ void wait_vmem() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 // 16 bytes stored non-temporal: a stream written once, kept from allocating in L2 and the memory-side cache.

@@ -110,13 +110,6 @@ struct KVTraits {
   }
 };
 
-// vmcnt(0): wait until this wave's vector memory operations (loads and stores) have completed.
-__device__ __forceinline__ void wait_vmem() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0x0F70);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
 __device__ __forceinline__ void store_agent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -683,13 +676,13 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
           bool nonfinite;
           const float scale = fp8_row_scale<R, VEC>(f, nonfinite);
           if (nonfinite && ok && c == 0 && p.status) atomicOr(p.status, kStatusNonFiniteRow);
-          uint32_t packed[4] = {0u, 0u, 0u, 0u};
+          // codes of clamp(x / scale, +-448); a zero or poisoned row (scale 0 or NaN) gets zero codes
+          float y[VEC];
 #pragma unroll
-          for (int i = 0; i < VEC; ++i) {
-            uint32_t code = 0u;
-            if (scale > 0.0f) code = f32_to_e4m3(fminf(fmaxf(f[i] / scale, -448.0f), 448.0f));
-            packed[i / 4] |= code << (8 * (i % 4));
-          }
+          for (int i = 0; i < VEC; ++i) y[i] = scale > 0.0f ? fminf(fmaxf(f[i] / scale, -448.0f), 448.0f) : 0.0f;
+          uint32_t packed[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) packed[i] = e4m3x4(y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]);
           const uint4 codes = make_uint4(packed[0], packed[1], packed[2], packed[3]);
           if (ok) {
             *reinterpret_cast<uint4*>(dst_base + off + c * VEC) = codes;

@@ -4,7 +4,8 @@
 // (dujunbaoV1/evaluation_wrapper.py:84-100, index_copy_ of the new rows at the current length), which
 // is bitwise the same cache content as HF DynamicLayer.update's torch.cat
 // (transformers/cache_utils.py:127-146). For fp8 caches the rows are quantized on write with one fp32
-// scale per (token, kv-head): scale = amax/448, q = e4m3(clamp(x / scale, -448, 448)).
+// scale per (token, kv-head): scale = amax/448, q = e4m3(clamp(x / scale, -448, 448)), the code from gfx950's
+// fp8 conversion instruction (round to nearest even).
 //
 // Grid (row blocks, sequences): a workgroup writes kAppendPasses passes of 256 / (D / 8) rows of one sequence
 // (K rows first, then V rows; head-major, then token), with every pass's source rows loaded before
@@ -31,31 +32,6 @@ struct AppendParams {
   int32_t num_kv_heads;
   int32_t n_new;
 };
-
-// Row offset (elements) of token t of sequence b, head h; returns false if the token has no slot.
-__device__ __forceinline__ bool append_row_offset(const KVLayout& c, int b, int h, int t, int64_t& row,
-                                                  int64_t& srow, int32_t* status) {
-  if (t < 0 || t >= c.max_tokens) {
-    if (status) atomicOr(status, kStatusAppendOverflow);
-    return false;
-  }
-  int64_t blk;
-  int tin;
-  if (c.block_table) {
-    blk = c.block_table[static_cast<int64_t>(b) * c.block_table_stride + t / c.page_size];
-    tin = t % c.page_size;
-    if (blk < 0 || blk >= c.num_blocks) {
-      if (status) atomicOr(status, kStatusBlockOutOfRange);
-      return false;
-    }
-  } else {
-    blk = b;
-    tin = t;
-  }
-  row = blk * c.stride_blk + h * c.stride_h + static_cast<int64_t>(tin) * c.stride_t;
-  srow = blk * c.scale_stride_blk + h * c.scale_stride_h + tin;
-  return true;
-}
 
 constexpr int kAppendPasses = 8;
 
@@ -100,16 +76,58 @@ __global__ __launch_bounds__(kBlockThreads) void kv_append_kernel(AppendParams p
   __syncthreads();
   const int pos = s_pos;
 
+  // Where every pass's row goes. Paged caches: the block ids of all passes are loaded together (each index
+  // clamped into the table), then checked, so that the passes do not wait for them one after another.
+  int64_t dst_row[kAppendPasses], dst_srow[kAppendPasses];
+  bool dst_ok[kAppendPasses];
+  {
+    int tok[kAppendPasses];
+    int64_t blk[kAppendPasses];
+#pragma unroll
+    for (int k = 0; k < kAppendPasses; ++k) {
+      const int r = min(first_row + k * ROWS_PER_PASS, rows_total - 1);
+      const int rr = r % rows_per_tensor;
+      tok[k] = pos + rr % p.n_new;
+    }
+    if (p.cache.block_table) {
+      const int32_t* const ids = p.cache.block_table + static_cast<int64_t>(b) * p.cache.block_table_stride;
+#pragma unroll
+      for (int k = 0; k < kAppendPasses; ++k) blk[k] = ids[min(max(tok[k], 0), p.cache.max_tokens - 1) / p.cache.page_size];
+    } else {
+#pragma unroll
+      for (int k = 0; k < kAppendPasses; ++k) blk[k] = b;
+    }
+    int32_t flags = 0;
+#pragma unroll
+    for (int k = 0; k < kAppendPasses; ++k) {
+      const int r = first_row + k * ROWS_PER_PASS;
+      const int h = (r % rows_per_tensor) / p.n_new;
+      const int t = tok[k];
+      const bool live = r < rows_total;
+      const bool in_cache = t >= 0 && t < p.cache.max_tokens;
+      const bool valid = blk[k] >= 0 && blk[k] < p.cache.num_blocks;
+      if (live && !in_cache) flags |= kStatusAppendOverflow;
+      else if (live && !valid) flags |= kStatusBlockOutOfRange;
+      dst_ok[k] = live && in_cache && valid;
+      const int tin = p.cache.block_table ? t % p.cache.page_size : t;
+      dst_row[k] = blk[k] * p.cache.stride_blk + h * p.cache.stride_h + static_cast<int64_t>(tin) * p.cache.stride_t;
+      dst_srow[k] = blk[k] * p.cache.scale_stride_blk + h * p.cache.scale_stride_h + tin;
+    }
+    if (flags && p.status && lane == 0) atomicOr(p.status, flags);
+  }
+  // 16-bit caches: every load (source rows, block ids) has been issued; wait for all of them once, so that no
+  // pass's stores are followed by a wait (behind the conditional stores the compiler's waits would cover the
+  // stores too). fp8 caches leave the waits per pass: their quantisation is the larger cost, and converting a
+  // pass while the later passes' rows are still arriving is worth more than the stores' waits.
+  if constexpr (KV_DT != kFP8E4M3) wait_vmem();
+
 #pragma unroll
   for (int k = 0; k < kAppendPasses; ++k) {
     const int r = first_row + k * ROWS_PER_PASS;
     if (r >= rows_total) continue;  // the whole row group (R lanes) skips together
     const int which = r / rows_per_tensor;
-    const int rr = r - which * rows_per_tensor;
-    const int h = rr / p.n_new;
-    const int j = rr - h * p.n_new;
-    int64_t row = 0, srow = 0;
-    const bool ok = append_row_offset(p.cache, b, h, pos + j, row, srow, p.status);
+    const int64_t row = dst_row[k], srow = dst_srow[k];
+    const bool ok = dst_ok[k];
     if constexpr (KV_DT == kFP8E4M3) {
       float f[VEC];
       unpack2<SRC_DT>(x[k].x, f[0], f[1]);
@@ -119,16 +137,11 @@ __global__ __launch_bounds__(kBlockThreads) void kv_append_kernel(AppendParams p
       bool nonfinite;
       const float scale = fp8_row_scale<R, VEC>(f, nonfinite);  // every lane of the row takes part
       if (nonfinite && ok && lane == 0 && p.status) atomicOr(p.status, kStatusNonFiniteRow);
-      uint32_t packed[2] = {0u, 0u};
+      // codes of clamp(x / scale, +-448); a zero or poisoned row (scale 0 or NaN) gets zero codes
+      float y[VEC];
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) {
-        uint32_t code = 0u;
-        if (scale > 0.0f) {
-          const float y = fminf(fmaxf(f[i] / scale, -448.0f), 448.0f);
-          code = f32_to_e4m3(y);
-        }
-        packed[i / 4] |= code << (8 * (i % 4));
-      }
+      for (int i = 0; i < VEC; ++i) y[i] = scale > 0.0f ? fminf(fmaxf(f[i] / scale, -448.0f), 448.0f) : 0.0f;
+      const uint32_t packed[2] = {e4m3x4(y[0], y[1], y[2], y[3]), e4m3x4(y[4], y[5], y[6], y[7])};
       if (ok) {
         uint8_t* dst = static_cast<uint8_t*>(which == 0 ? p.cache.k : p.cache.v) + row + lane * VEC;
         *reinterpret_cast<uint2*>(dst) = make_uint2(packed[0], packed[1]);

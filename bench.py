@@ -61,7 +61,8 @@ MALL_BYTES = 256 << 20
 def parse_args(argv=None):
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--config", choices=("c1", "c2", "c3", "c4", "c5", "model", "microbench", "calib", "gather"),
+    p.add_argument("--config", choices=("c1", "c2", "c3", "c4", "c5", "model", "microbench", "calib", "gather",
+                                        "prefill"),
                    default="c2",
                    help="model: the whole text-decoder step per generated token; microbench: the shape of the "
                         "reference's published decode microbenchmark (both reported separately)")
@@ -623,6 +624,121 @@ def gather(args) -> int:
     return 0 if max_err == 0 else 1
 
 
+def prefill(args) -> int:
+    """--config prefill: the prefill writer, one aicas_kv_append launch that writes a 2048-token prompt for each
+    of 32 sequences (8 kv heads, head_dim 128) into the C5 layout (16-token pages over a permuted block table,
+    fp8 e4m3 quantised on write with an fp32 scale per (token, kv head)), and the same into a contiguous bf16
+    cache. Bytes per launch: the bf16 rows read plus the cache rows (and scales) written. Two distinct caches
+    alternate in the graph; µs per launch = graph time / launches. The CPU baseline is the oracle's quantisation
+    and paged scatter of the same rows (torch on the host cores) over a bounded sample of the sequences."""
+    import torch
+
+    from aicas_amd import ops
+    from aicas_amd.workloads import HEAD_DIM as D, HKV, PAGE, generator, normal
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    B, N, NL, reps = 32, 2048, 2, args.steps or 20
+    gen = generator(dev, 6)
+    k_src = normal((B, HKV, N, D), gen, dev, outlier_frac=0.01)
+    v_src = normal((B, HKV, N, D), gen, dev, outlier_frac=0.01)
+    pos = torch.zeros(B, dtype=torch.int32, device=dev)
+    per_seq = N // PAGE
+    paged, dense = [], []
+    for _ in range(NL):
+        bt = torch.randperm(B * per_seq, generator=gen, device=dev).to(torch.int32).view(B, per_seq)
+        kp = torch.zeros((B * per_seq, HKV, PAGE, D), dtype=ops.FP8_DTYPE, device=dev)
+        ks = torch.zeros((B * per_seq, HKV, PAGE), dtype=torch.float32, device=dev)
+        paged.append(ops.KVCacheView(kp, torch.zeros_like(kp), ks, torch.zeros_like(ks), bt))
+        kd = torch.zeros((B, HKV, N, D), dtype=torch.bfloat16, device=dev)
+        dense.append(ops.KVCacheView(kd, torch.zeros_like(kd)))
+    stream = torch.cuda.Stream(device=dev)
+
+    def per_launch_us(views):
+        with torch.cuda.stream(stream):
+            for v in views:
+                ops.kv_append(v, k_src, v_src, pos)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                for v in views:
+                    ops.kv_append(v, k_src, v_src, pos)
+            for _ in range(3):
+                graph.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (reps * len(views))
+
+    rows = 2 * B * HKV * N
+    fp8_bytes = rows * D * 2 + rows * (D + 4)
+    bf16_bytes = rows * D * 2 * 2
+    us_fp8 = per_launch_us(paged)
+    us_bf16 = per_launch_us(dense)
+
+    # parity of the paged fp8 cache against the oracle's quantisation, a few sequences
+    from oracle import reference_path as ref
+
+    view = paged[-1]
+    kc, ksc, btc = view.k.cpu(), view.k_scale.cpu(), view.block_table.cpu()
+    mismatched = 0
+    for b in (0, B - 1):
+        codes, scale = ref.fp8_quantize_rows(k_src[b].cpu().float())
+        got = ref.paged_gather(kc, btc[b : b + 1], [N])[0]
+        got_s = ref.paged_gather(ksc[..., None], btc[b : b + 1], [N])[0][..., 0]
+        mismatched += int((got.view(torch.uint8) != codes.view(torch.uint8)).sum())
+        mismatched += int((got_s != scale).sum())
+
+    cpu = None
+    if args.cpu_baseline_seconds > 0:
+        threads, core_info = host_cores()
+        torch.set_num_threads(threads)
+        src = (k_src.cpu(), v_src.cpu())
+        pool = torch.zeros((per_seq, HKV, PAGE, D), dtype=ops.FP8_DTYPE)
+        spool = torch.zeros((per_seq, HKV, PAGE), dtype=torch.float32)
+        table = torch.arange(per_seq, dtype=torch.int32)[None]
+        t_s, done = time.perf_counter(), 0
+        for b in range(B):
+            for x in src:
+                codes, scale = ref.fp8_quantize_rows(x[b].float())
+                for t in range(0, N, PAGE):  # one page of rows at a time into its block
+                    blk = int(table[0, t // PAGE])
+                    pool[blk] = codes[:, t : t + PAGE]
+                    spool[blk] = scale[:, t : t + PAGE]
+            done += 1
+            if time.perf_counter() - t_s > args.cpu_baseline_seconds:
+                break
+        cpu_us = (time.perf_counter() - t_s) / done * B * 1e6
+        cpu = {"value": round(cpu_us, 1), "unit": "us/launch", "cores": threads, **core_info, "kind": "port",
+               "sample": f"the oracle's fp8 quantisation + paged scatter (torch {torch.__version__}, host) of "
+                         f"{done} of the {B} sequences, scaled to all {B}"}
+    gbps = fp8_bytes / (us_fp8 * 1e-6) / 1e9
+    result = {
+        "metric": "us per aicas_kv_append prefill launch & achieved HBM GB/s (% of 8 TB/s): a 2048-token prompt "
+                  "for 32 sequences into the C5 paged fp8 layout (reported beside the headline, not the headline)",
+        "value": round(us_fp8, 2), "unit": "us/launch", "n_gpus": 1, "steps": reps, "warmup": 3,
+        "ms_per_step": round(us_fp8 / 1e3, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16->fp8", "data": "synthetic (seeded N(0,1), 1% outliers +-8)",
+        "config": {"workload": f"kv append (prefill): B={B}, 8 kv heads, head_dim 128, {N} new tokens per "
+                               "sequence, 16-token pages, fp8 e4m3 + fp32 scales", "batch": B, "new_tokens": N,
+                   "cache_instances": NL},
+        "roofline": {"bound": "hbm", "kernel": "kv_append_kernel<bf16,fp8,D=128>", "achieved": round(gbps, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "bytes_per_launch": fp8_bytes, "avg_launch_us": round(us_fp8, 3)},
+        "contiguous_bf16": {"us_per_launch": round(us_bf16, 2), "bytes_per_launch": bf16_bytes,
+                            "gbps": round(bf16_bytes / (us_bf16 * 1e-6) / 1e9, 1),
+                            "frac_of_8tbps": round(bf16_bytes / (us_bf16 * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)},
+        "cpu_baseline": cpu,
+        "parity_mismatched_elements": mismatched,
+    }
+    print(json.dumps(result), flush=True)
+    return 0 if mismatched == 0 else 1
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.config == "model" and args.gpus == 1:
@@ -633,6 +749,8 @@ def main(argv=None) -> int:
         return calib(args)
     if args.config == "gather" and args.gpus == 1:
         return gather(args)
+    if args.config == "prefill" and args.gpus == 1:
+        return prefill(args)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: each GPU serves its own "
               "sequences (or kv heads), so the step does not shard across GPUs here.", file=sys.stderr)
