@@ -185,3 +185,51 @@ def test_merge_paths_every_group_shape(dev, D, G):
     base = outs[counts[0]]
     for n in counts[1:]:
         assert (outs[n] - base).abs().max() <= 2.0 ** -7 * base.abs().max(), n
+
+
+@pytest.mark.parametrize("name, B, lens, tps, fp8, page", [
+    ("uniform 4 splits", 8, [2048] * 8, 0, False, 0),
+    ("ragged split sizes", 4, [100, 5000, 40, 3000], 64, False, 0),
+    ("paged fp8 ragged", 6, [300, 4100, 2000, 17, 6000, 900], 0, True, 16),
+])
+def test_replay_soak_few_splits(dev, name, B, lens, tps, fp8, page):
+    """A correctness soak (not aimed at any known failure) of merges of few splits (the headline's shape among
+    them): the plain decode captured once and replayed back to back; every replay's output equals the first's
+    bit for bit (stops at the first mismatch), the counters end at zero, and the output matches the oracle."""
+    gen = torch.Generator(device=dev).manual_seed(21 + len(lens))
+    view, q, kn, vn, pos = _case(dev, gen, B, 16, 8, 128, lens, fp8=fp8, page=page)
+    ws = torch.zeros(8 << 20, dtype=torch.uint8, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    stream = torch.cuda.Stream(device=dev)
+    n = 200
+    hist = torch.empty((n,) + tuple(q.shape), dtype=q.dtype, device=dev)
+    with torch.cuda.stream(stream):
+        ops.decode_attention(q, view, sm_scale=128 ** -0.5, seq_lens=pos, max_seq_len=max(lens), out=out,
+                             tokens_per_split=tps, workspace=ws, status=status)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            ops.decode_attention(q, view, sm_scale=128 ** -0.5, seq_lens=pos, max_seq_len=max(lens), out=out,
+                                 tokens_per_split=tps, workspace=ws, status=status)
+        for i in range(n):
+            graph.replay()
+            hist[i].copy_(out)
+        torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    first = _bits(hist[0])
+    for i in range(1, n):
+        assert torch.equal(_bits(hist[i]), first), f"replay {i} differs from replay 0"
+    assert int(ws[:COUNTER_BYTES].count_nonzero()) == 0
+    b = max(range(B), key=lambda j: lens[j])
+    L = lens[b]
+    if page:
+        bt = view.block_table[b : b + 1].cpu()
+        k = ref.paged_gather(view.k.cpu(), bt, [L])[0].float()
+        v = ref.paged_gather(view.v.cpu(), bt, [L])[0].float()
+        k = k * ref.paged_gather(view.k_scale.cpu()[..., None], bt, [L])[0]
+        v = v * ref.paged_gather(view.v_scale.cpu()[..., None], bt, [L])[0]
+    else:
+        k, v = view.k[b, :, :L].cpu(), view.v[b, :, :L].cpu()
+    expect = ref.decode_fp64(q[b : b + 1].cpu(), k[None], v[None], 128 ** -0.5, 2)
+    assert (hist[0][b : b + 1].double().cpu() - expect).abs().max().item() <= (6e-2 if fp8 else 2e-2)
