@@ -146,9 +146,10 @@ int make_layout(const aicas_kv_cache_t* c, int32_t batch, int32_t num_kv_heads, 
 // (the append kernel only bumps in place when one workgroup owns the sequence).
 template <int SRC, int KV>
 int launch_append_d(const aicas::AppendParams& p, int32_t batch, int32_t head_dim, hipStream_t s) {
+  // the kernel indexes a sequence's rows with 31-bit integers
   const int64_t rows = 2 * int64_t{p.num_kv_heads} * p.n_new;
+  if (rows > INT32_MAX) return fail(AICAS_ERR_UNSUPPORTED, "too many rows (%lld) in one append", (long long)rows);
   const int64_t blocks = ceil_div(rows, aicas::append_rows_per_workgroup(head_dim));
-  if (blocks > INT32_MAX) return fail(AICAS_ERR_UNSUPPORTED, "too many rows (%lld) in one append", (long long)rows);
   const dim3 grid(static_cast<uint32_t>(blocks), batch), block(aicas::kBlockThreads);
   switch (head_dim) {
     case 16: hipLaunchKernelGGL((aicas::kv_append_kernel<SRC, KV, 16>), grid, block, 0, s, p); break;
@@ -541,6 +542,8 @@ int aicas_kv_append(const aicas_kv_cache_t* cache, int32_t src_dtype, const void
   p.status = status;
   p.num_kv_heads = num_kv_heads;
   p.n_new = n_new;
+  p.div_n_new = aicas::fast_div_make(static_cast<uint32_t>(n_new));
+  p.page_shift = cache->block_table ? ilog2(cache->page_size) : 0;
   using namespace aicas;
   if (src_dtype == kBF16) {
     if (cache->kv_dtype == kFP8E4M3) return launch_append_d<kBF16, kFP8E4M3>(p, batch, head_dim, stream);

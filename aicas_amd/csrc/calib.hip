@@ -1,8 +1,12 @@
 // Calibration and self-check kernels (libaicas_calib.so; not part of the decode ABI).
 //
 // aicas_calib_fp8_encoder_check: the fp8 encoding the kernels use (e4m3x4, gfx950's v_cvt_pk_fp8_f32) against
-// the encoder written out from the format (f32_to_e4m3) on every float with |x| <= 448; a GPU test requires
-// zero mismatches.
+// the encoder written out from the format (f32_to_e4m3) on every float with |x| <= 448;
+// aicas_calib_fp8_divide_check: the kernels' fp8 row quantiser (fp8_quantize: one reciprocal per row and a
+// corrected product per value) against the codes of the IEEE quotient, for every (row maximum, value) pair of
+// a 16-bit source type;
+// aicas_calib_fast_div_check: the launch-constant integer division (fast_div) against the division.
+// GPU tests require zero mismatches from each.
 //
 // Bandwidth calibration for bench.py --config calib:
 // They read exactly the bytes one decode launch of a contiguous bf16 cache reads (K and V rows of B sequences x
@@ -101,6 +105,54 @@ __global__ __launch_bounds__(aicas::kBlockThreads) void fp8_encoder_check_kernel
   if (bad) atomicAdd(mismatches, bad);
 }
 
+// Block i takes the row maximum amax = the (i + 1)-th positive 16-bit pattern of DT (every one is finite for the
+// grid the host launches) and scale s = amax / 448, as fp8_row_scale gives it; thread t the 256 values with
+// patterns 256 t .. 256 t + 255, 4 at a time, those not finite or above amax in magnitude taken as 0.
+template <int DT>
+__global__ __launch_bounds__(aicas::kBlockThreads) void fp8_divide_check_kernel(unsigned long long* mismatches,
+                                                                               uint32_t* first) {
+  const uint32_t amax_bits = blockIdx.x + 1;
+  float amax, unused;
+  aicas::unpack2<DT>(amax_bits, amax, unused);
+  const float s = amax / 448.0f;
+  unsigned long long bad = 0;
+  for (int g = 0; g < 64; ++g) {
+    const uint32_t base = threadIdx.x * 256u + 4u * g;
+    float x[4], y[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float v;
+      aicas::unpack2<DT>(base + j, v, unused);
+      x[j] = fabsf(v) <= amax ? v : 0.0f;
+      y[j] = fminf(fmaxf(x[j] / s, -448.0f), 448.0f);
+    }
+    uint32_t codes;
+    aicas::fp8_quantize<4>(x, s, &codes);
+    if (codes != aicas::e4m3x4(y[0], y[1], y[2], y[3])) {
+      ++bad;
+      atomicCAS(first, 0xffffffffu, (amax_bits << 16) | base);
+    }
+  }
+  if (bad) atomicAdd(mismatches, bad);
+}
+
+// Thread g of 2^24 divides g and 2^31 - 1 - 127 g (the whole non-negative 31-bit range, sparsely) by d.
+__global__ __launch_bounds__(aicas::kBlockThreads) void fast_div_check_kernel(int32_t d, aicas::FastDiv f,
+                                                                             unsigned long long* mismatches,
+                                                                             uint32_t* first) {
+  const uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
+  const int32_t xs[2] = {static_cast<int32_t>(g), static_cast<int32_t>(0x7fffffffu - 127u * g)};
+  unsigned long long bad = 0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    if (aicas::fast_div(xs[i], f) != xs[i] / d) {
+      ++bad;
+      atomicCAS(first, 0xffffffffu, static_cast<uint32_t>(d));
+    }
+  }
+  if (bad) atomicAdd(mismatches, bad);
+}
+
 }  // namespace
 
 extern "C" {
@@ -134,6 +186,44 @@ int aicas_calib_fp8_encoder_check(unsigned long long* mismatches, uint32_t* firs
   for (uint32_t slice = 0; slice < 16; ++slice) {
     hipLaunchKernelGGL(fp8_encoder_check_kernel, dim3((1u << 24) / aicas::kBlockThreads), dim3(aicas::kBlockThreads),
                        0, stream, slice, mismatches, first_pattern);
+    if (hipGetLastError() != hipSuccess) return 2;
+  }
+  return hipStreamSynchronize(stream) == hipSuccess ? 0 : 2;
+}
+
+// src_dtype 0 (bf16) or 1 (fp16): every positive finite row maximum and every value of that type through
+// fp8_quantize and through the IEEE quotient's codes; *mismatches (zeroed here) counts the groups of 4 values
+// whose codes differ, *first_pattern (0xffffffff here) holds (amax pattern << 16 | value pattern) of the first.
+// Synchronous.
+int aicas_calib_fp8_divide_check(int32_t src_dtype, unsigned long long* mismatches, uint32_t* first_pattern,
+                                 hipStream_t stream) {
+  if (!mismatches || !first_pattern || (src_dtype != aicas::kBF16 && src_dtype != aicas::kFP16)) return 1;
+  if (hipMemsetAsync(mismatches, 0, sizeof(unsigned long long), stream) != hipSuccess) return 2;
+  if (hipMemsetAsync(first_pattern, 0xff, sizeof(uint32_t), stream) != hipSuccess) return 2;
+  // positive finite patterns: bf16 0x0001 .. 0x7f7f, fp16 0x0001 .. 0x7bff
+  if (src_dtype == aicas::kBF16)
+    hipLaunchKernelGGL(fp8_divide_check_kernel<aicas::kBF16>, dim3(0x7f7f), dim3(aicas::kBlockThreads), 0, stream,
+                       mismatches, first_pattern);
+  else
+    hipLaunchKernelGGL(fp8_divide_check_kernel<aicas::kFP16>, dim3(0x7bff), dim3(aicas::kBlockThreads), 0, stream,
+                       mismatches, first_pattern);
+  if (hipGetLastError() != hipSuccess) return 2;
+  return hipStreamSynchronize(stream) == hipSuccess ? 0 : 2;
+}
+
+// Each of the n divisors (host array, each >= 1) with its multiplier from fast_div_make, against the division on
+// 2^25 dividends; *mismatches (zeroed here) counts the differences, *first_divisor (0xffffffff here) the first
+// divisor that had one. Synchronous.
+int aicas_calib_fast_div_check(const int32_t* divisors, int32_t n, unsigned long long* mismatches,
+                               uint32_t* first_divisor, hipStream_t stream) {
+  if (!divisors || n <= 0 || !mismatches || !first_divisor) return 1;
+  if (hipMemsetAsync(mismatches, 0, sizeof(unsigned long long), stream) != hipSuccess) return 2;
+  if (hipMemsetAsync(first_divisor, 0xff, sizeof(uint32_t), stream) != hipSuccess) return 2;
+  for (int32_t i = 0; i < n; ++i) {
+    if (divisors[i] < 1) return 1;
+    hipLaunchKernelGGL(fast_div_check_kernel, dim3((1u << 24) / aicas::kBlockThreads), dim3(aicas::kBlockThreads), 0,
+                       stream, divisors[i], aicas::fast_div_make(static_cast<uint32_t>(divisors[i])), mismatches,
+                       first_divisor);
     if (hipGetLastError() != hipSuccess) return 2;
   }
   return hipStreamSynchronize(stream) == hipSuccess ? 0 : 2;

@@ -181,6 +181,63 @@ __device__ __forceinline__ float fp8_row_scale(const float* f, bool& nonfinite) 
   return nonfinite ? __builtin_nanf("") : amax / 448.0f;
 }
 
+// Row scales at or above this take the one-reciprocal division in fp8_quantize.
+constexpr float kFp8FastDivMinScale = 0x1p-90f;
+
+// The e4m3 codes of VEC finite values of one fp8 cache row with scale s (fp8_row_scale): clamp(x / s, +-448)
+// encoded by e4m3x4, code i in byte i % 4 of packed[i / 4]; a zero or poisoned row (s not > 0) gets zero codes.
+// The quotient is x / s correctly rounded, from one division per row: y = 1 / s (IEEE), then per value
+// q0 = x * y and one correction q = q0 + (x - s q0) y with the residual exact in an FMA — Markstein's theorem
+// (y the correctly rounded reciprocal and q0 within an ulp of x / s make q the correctly rounded quotient) —
+// provided the residual does not underflow; the sign is then x's (the correction would give +0 for -0). For
+// s >= 2^-90 that holds whenever |x / s| >= 2^-11, and smaller quotients encode to a zero of x's sign whatever
+// their last bits; smaller scales divide value by value. So the codes are
+// those of the IEEE quotient for every input, which libaicas_calib.so's aicas_calib_fp8_divide_check compares
+// over every (row maximum, value) pair of both 16-bit source types.
+template <int VEC>
+__device__ __forceinline__ void fp8_quantize(const float* f, float s, uint32_t* packed) {
+  float y[VEC];
+  if (s >= kFp8FastDivMinScale) {
+    const float r = 1.0f / s;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      const float q0 = f[i] * r;
+      // the correction's sum turns a -0 quotient into +0: the quotient has the sign of x (s > 0)
+      const float q = copysignf(fmaf(fmaf(-q0, s, f[i]), r, q0), f[i]);
+      y[i] = fminf(fmaxf(q, -448.0f), 448.0f);
+    }
+  } else if (s > 0.0f) {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) y[i] = fminf(fmaxf(f[i] / s, -448.0f), 448.0f);
+  } else {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) y[i] = 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < VEC / 4; ++i) packed[i] = e4m3x4(y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]);
+}
+
+// Division by a divisor d >= 1 fixed for a launch, for dividends 0 <= x < 2^31 (Granlund and Montgomery's
+// round-up method): with l = ceil(log2 d) and m = floor(2^32 (2^l - d) / d) + 1, x / d = (umulhi(x, m) + x) >> l,
+// where the sum stays below 2^32 because x < 2^31. libaicas_calib.so's aicas_calib_fast_div_check compares it
+// with the division on the GPU.
+struct FastDiv {
+  uint32_t m;
+  uint32_t l;
+};
+
+inline FastDiv fast_div_make(uint32_t d) {
+  uint32_t l = 0;
+  while ((uint64_t{1} << l) < d) ++l;
+  const uint64_t m = ((uint64_t{1} << 32) * ((uint64_t{1} << l) - d)) / d + 1;
+  return FastDiv{static_cast<uint32_t>(m), l};
+}
+
+__device__ __forceinline__ int fast_div(int x, FastDiv f) {
+  const uint32_t u = static_cast<uint32_t>(x);
+  return static_cast<int>((__umulhi(u, f.m) + u) >> f.l);
+}
+
 // A 16-byte load of data read once per launch (cache rows): non-temporal (global_load_dwordx4 ... nt), so the
 // stream does not allocate in the caches on its way through. The decode kernel's access pattern as a pure read
 // (B=8 L=2112, 69 MB): 12.4 us per launch with these loads, 13.5 with plain ones.

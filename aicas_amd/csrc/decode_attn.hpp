@@ -676,13 +676,8 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
           bool nonfinite;
           const float scale = fp8_row_scale<R, VEC>(f, nonfinite);
           if (nonfinite && ok && c == 0 && p.status) atomicOr(p.status, kStatusNonFiniteRow);
-          // codes of clamp(x / scale, +-448); a zero or poisoned row (scale 0 or NaN) gets zero codes
-          float y[VEC];
-#pragma unroll
-          for (int i = 0; i < VEC; ++i) y[i] = scale > 0.0f ? fminf(fmaxf(f[i] / scale, -448.0f), 448.0f) : 0.0f;
           uint32_t packed[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) packed[i] = e4m3x4(y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]);
+          fp8_quantize<VEC>(f, scale, packed);  // the codes kv_append_kernel writes
           const uint4 codes = make_uint4(packed[0], packed[1], packed[2], packed[3]);
           if (ok) {
             *reinterpret_cast<uint4*>(dst_base + off + c * VEC) = codes;

@@ -5,7 +5,7 @@
 // is bitwise the same cache content as HF DynamicLayer.update's torch.cat
 // (transformers/cache_utils.py:127-146). For fp8 caches the rows are quantized on write with one fp32
 // scale per (token, kv-head): scale = amax/448, q = e4m3(clamp(x / scale, -448, 448)), the code from gfx950's
-// fp8 conversion instruction (round to nearest even).
+// fp8 conversion instruction (round to nearest even) of the correctly rounded quotient (fp8_quantize).
 //
 // Grid (row blocks, sequences): a workgroup writes kAppendPasses passes of 256 / (D / 8) rows of one sequence
 // (K rows first, then V rows; head-major, then token), with every pass's source rows loaded before
@@ -31,6 +31,8 @@ struct AppendParams {
   int32_t* status;
   int32_t num_kv_heads;
   int32_t n_new;
+  FastDiv div_n_new;   // division by n_new
+  int32_t page_shift;  // paged caches: log2(page_size)
 };
 
 constexpr int kAppendPasses = 8;
@@ -54,12 +56,18 @@ __global__ __launch_bounds__(kBlockThreads) void kv_append_kernel(AppendParams p
   const int rows_total = 2 * rows_per_tensor;
   const int first_row = blockIdx.x * ROWS_PER_PASS * kAppendPasses + tid / R;
 
-  // Source row r (K rows first, then V rows; head-major, then token).
-  auto src_row = [&](int r) -> const uint16_t* {
-    const int which = r / rows_per_tensor;
+  // Row r of the launch's 0 <= r < rows_total (K rows first, then V rows; head-major, then token): tensor
+  // `which`, kv head h, new row j (a division by n_new with the launch's multiplier: per-lane integer
+  // divisions by launch values were most of this kernel's instructions).
+  auto row_coords = [&](int r, int& which, int& h, int& j) {
+    which = r >= rows_per_tensor ? 1 : 0;
     const int rr = r - which * rows_per_tensor;
-    const int h = rr / p.n_new;
-    const int j = rr - h * p.n_new;
+    h = fast_div(rr, p.div_n_new);
+    j = rr - h * p.n_new;
+  };
+  auto src_row = [&](int r) -> const uint16_t* {
+    int which, h, j;
+    row_coords(r, which, h, j);
     return which == 0 ? static_cast<const uint16_t*>(p.k_src) + b * p.k_src_stride_b + h * p.k_src_stride_h +
                             j * p.k_src_stride_t
                       : static_cast<const uint16_t*>(p.v_src) + b * p.v_src_stride_b + h * p.v_src_stride_h +
@@ -81,27 +89,28 @@ __global__ __launch_bounds__(kBlockThreads) void kv_append_kernel(AppendParams p
   int64_t dst_row[kAppendPasses], dst_srow[kAppendPasses];
   bool dst_ok[kAppendPasses];
   {
-    int tok[kAppendPasses];
+    int tok[kAppendPasses], head[kAppendPasses];
     int64_t blk[kAppendPasses];
 #pragma unroll
     for (int k = 0; k < kAppendPasses; ++k) {
-      const int r = min(first_row + k * ROWS_PER_PASS, rows_total - 1);
-      const int rr = r % rows_per_tensor;
-      tok[k] = pos + rr % p.n_new;
+      int which, j;
+      row_coords(min(first_row + k * ROWS_PER_PASS, rows_total - 1), which, head[k], j);
+      tok[k] = pos + j;
     }
     if (p.cache.block_table) {
       const int32_t* const ids = p.cache.block_table + static_cast<int64_t>(b) * p.cache.block_table_stride;
 #pragma unroll
-      for (int k = 0; k < kAppendPasses; ++k) blk[k] = ids[min(max(tok[k], 0), p.cache.max_tokens - 1) / p.cache.page_size];
+      for (int k = 0; k < kAppendPasses; ++k) blk[k] = ids[min(max(tok[k], 0), p.cache.max_tokens - 1) >> p.page_shift];
     } else {
 #pragma unroll
       for (int k = 0; k < kAppendPasses; ++k) blk[k] = b;
     }
+    const int page_mask = (1 << p.page_shift) - 1;
     int32_t flags = 0;
 #pragma unroll
     for (int k = 0; k < kAppendPasses; ++k) {
       const int r = first_row + k * ROWS_PER_PASS;
-      const int h = (r % rows_per_tensor) / p.n_new;
+      const int h = head[k];
       const int t = tok[k];
       const bool live = r < rows_total;
       const bool in_cache = t >= 0 && t < p.cache.max_tokens;
@@ -109,7 +118,7 @@ __global__ __launch_bounds__(kBlockThreads) void kv_append_kernel(AppendParams p
       if (live && !in_cache) flags |= kStatusAppendOverflow;
       else if (live && !valid) flags |= kStatusBlockOutOfRange;
       dst_ok[k] = live && in_cache && valid;
-      const int tin = p.cache.block_table ? t % p.cache.page_size : t;
+      const int tin = p.cache.block_table ? t & page_mask : t;
       dst_row[k] = blk[k] * p.cache.stride_blk + h * p.cache.stride_h + static_cast<int64_t>(tin) * p.cache.stride_t;
       dst_srow[k] = blk[k] * p.cache.scale_stride_blk + h * p.cache.scale_stride_h + tin;
     }
@@ -125,7 +134,7 @@ __global__ __launch_bounds__(kBlockThreads) void kv_append_kernel(AppendParams p
   for (int k = 0; k < kAppendPasses; ++k) {
     const int r = first_row + k * ROWS_PER_PASS;
     if (r >= rows_total) continue;  // the whole row group (R lanes) skips together
-    const int which = r / rows_per_tensor;
+    const int which = r >= rows_per_tensor ? 1 : 0;
     const int64_t row = dst_row[k], srow = dst_srow[k];
     const bool ok = dst_ok[k];
     if constexpr (KV_DT == kFP8E4M3) {
@@ -137,11 +146,8 @@ __global__ __launch_bounds__(kBlockThreads) void kv_append_kernel(AppendParams p
       bool nonfinite;
       const float scale = fp8_row_scale<R, VEC>(f, nonfinite);  // every lane of the row takes part
       if (nonfinite && ok && lane == 0 && p.status) atomicOr(p.status, kStatusNonFiniteRow);
-      // codes of clamp(x / scale, +-448); a zero or poisoned row (scale 0 or NaN) gets zero codes
-      float y[VEC];
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) y[i] = scale > 0.0f ? fminf(fmaxf(f[i] / scale, -448.0f), 448.0f) : 0.0f;
-      const uint32_t packed[2] = {e4m3x4(y[0], y[1], y[2], y[3]), e4m3x4(y[4], y[5], y[6], y[7])};
+      uint32_t packed[2];
+      fp8_quantize<VEC>(f, scale, packed);
       if (ok) {
         uint8_t* dst = static_cast<uint8_t*>(which == 0 ? p.cache.k : p.cache.v) + row + lane * VEC;
         *reinterpret_cast<uint2*>(dst) = make_uint2(packed[0], packed[1]);

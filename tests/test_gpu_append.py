@@ -146,6 +146,52 @@ def test_append_paged_bitexact(dev, status, fp8):
     assert int(status.item()) == 0
 
 
+@pytest.mark.parametrize("n_new, H, page", [(1, 1, 1), (2, 3, 2), (5, 8, 4), (7, 2, 16), (16, 8, 16),
+                                             (33, 5, 64), (300, 3, 32), (1000, 1, 128)])
+@pytest.mark.parametrize("fp8", [False, True])
+def test_append_paged_row_indexing_shapes(dev, status, n_new, H, page, fp8):
+    """The append kernel finds each row's head and token by dividing its index by the launch's new-row count (a
+    multiplier computed on the host) and its page by a shift: over new-row counts, head counts and page sizes
+    whose rows straddle workgroups, heads and pages in every way, every row lands bit for bit where the oracle
+    scatters it (bf16, and fp8 codes and scales)."""
+    B, D = 3, 64
+    g = torch.Generator().manual_seed(1000 * n_new + 10 * H + page)
+    lens = [0, 5, 3 * page + 1]
+    per_seq = -(-(max(lens) + n_new) // page)
+    nblocks = B * per_seq + 2
+    bt = torch.randperm(nblocks, generator=g)[: B * per_seq].to(torch.int32).view(B, per_seq)
+    k_new = torch.randn((B, H, n_new, D), generator=g).to(torch.bfloat16)
+    v_new = torch.randn((B, H, n_new, D), generator=g).to(torch.bfloat16)
+    store = ops.FP8_DTYPE if fp8 else torch.bfloat16
+    pk = torch.zeros((nblocks, H, page, D), dtype=store)
+    pv = torch.zeros_like(pk)
+    sk = torch.zeros((nblocks, H, page)) if fp8 else None
+    sv = torch.zeros((nblocks, H, page)) if fp8 else None
+    ek, ev = pk.clone(), pv.clone()
+    esk = sk.clone() if fp8 else None
+    esv = sv.clone() if fp8 else None
+    kr, vr = (ref.fp8_quantize_rows(k_new), ref.fp8_quantize_rows(v_new)) if fp8 else ((k_new, None), (v_new, None))
+    for b, L in enumerate(lens):
+        for j in range(n_new):
+            ref.paged_scatter_rows(ek, bt, b, L + j, kr[0][b, :, j])
+            ref.paged_scatter_rows(ev, bt, b, L + j, vr[0][b, :, j])
+            if fp8:
+                ref.paged_scatter_rows(esk, bt, b, L + j, kr[1][b, :, j])
+                ref.paged_scatter_rows(esv, bt, b, L + j, vr[1][b, :, j])
+    view = ops.KVCacheView(pk.to(dev), pv.to(dev), sk.to(dev) if fp8 else None, sv.to(dev) if fp8 else None,
+                           bt.to(dev))
+    pos = torch.tensor(lens, dtype=torch.int32, device=dev)
+    ops.kv_append(view, k_new.to(dev), v_new.to(dev), pos, pos, status)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(view.k.cpu()), _bits(ek))
+    assert torch.equal(_bits(view.v.cpu()), _bits(ev))
+    if fp8:
+        assert torch.equal(view.k_scale.cpu(), esk)
+        assert torch.equal(view.v_scale.cpu(), esv)
+    assert pos.cpu().tolist() == [L + n_new for L in lens]
+    assert int(status.item()) == 0
+
+
 def test_append_overflow_is_dropped_and_reported(dev, status):
     B, H, D, cap = 2, 2, 64, 8
     gk = torch.zeros((B, H, cap, D), dtype=torch.bfloat16, device=dev)

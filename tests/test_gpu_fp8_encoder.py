@@ -1,9 +1,13 @@
-"""The fp8 encoding of the append kernels.
+"""The fp8 encoding of the append kernels, and the launch-constant integer division of the append kernel.
 
 The kernels quantise with gfx950's fp8 conversion instruction (e4m3x4). Exhaustively, on every float with
 |x| <= 448 (the clamped domain the kernels feed it), it must give the codes of the encoder written out from the
-OCP e4m3 format (round to nearest even). And on rows of every magnitude, through the product's own append, the
-codes and scales must be the oracle's (torch's cast of clamp(x / scale)).
+OCP e4m3 format (round to nearest even). The quotient x / scale comes from one reciprocal per row and a
+corrected product per value (fp8_quantize); for every (row maximum, value) pair of bf16 and of fp16 sources its
+codes must be those of the IEEE quotient. On rows of every magnitude, through the product's own append, codes and
+scales must be the oracle's (torch's cast of clamp(x / scale)). The append kernel divides row indexes by the
+launch's new-row count with a multiplier (fast_div); on 2^25 dividends spread over the 31-bit range it must
+equal the division for every divisor tried.
 """
 
 import ctypes
@@ -27,6 +31,35 @@ def test_hardware_encoder_matches_format_encoder_on_every_float(dev):
     rc = lib.aicas_calib_fp8_encoder_check(mism.data_ptr(), first.data_ptr(), stream.cuda_stream)
     assert rc == 0
     assert int(mism.item()) == 0, f"first differing pattern {int(first.item()) & 0xffffffff:#010x}"
+
+
+@pytest.mark.parametrize("src_dtype, name", [(0, "bf16"), (1, "fp16")])
+def test_row_quantiser_gives_the_ieee_quotient_codes(dev, src_dtype, name):
+    lib = ctypes.CDLL(CALIB_OUTPUT, mode=ctypes.RTLD_LOCAL)
+    lib.aicas_calib_fp8_divide_check.argtypes = [ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    mism = torch.zeros(1, dtype=torch.int64, device=dev)
+    first = torch.zeros(1, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    assert lib.aicas_calib_fp8_divide_check(src_dtype, mism.data_ptr(), first.data_ptr(), stream.cuda_stream) == 0
+    f = int(first.item()) & 0xffffffff
+    assert int(mism.item()) == 0, f"{name}: row maximum {f >> 16:#06x}, values from {f & 0xffff:#06x}"
+
+
+def test_launch_constant_division(dev):
+    divisors = list(range(1, 4097)) + [1 << k for k in range(13, 31)]
+    divisors += [(1 << k) + e for k in range(13, 31) for e in (-1, 1)] + [3 * 2048 * 8, 6000, 65535, 65537,
+                                                                           1000003, 123456789, 2147483647]
+    arr = (ctypes.c_int32 * len(divisors))(*divisors)
+    lib = ctypes.CDLL(CALIB_OUTPUT, mode=ctypes.RTLD_LOCAL)
+    lib.aicas_calib_fast_div_check.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p,
+                                               ctypes.c_void_p]
+    mism = torch.zeros(1, dtype=torch.int64, device=dev)
+    first = torch.zeros(1, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    rc = lib.aicas_calib_fast_div_check(ctypes.cast(arr, ctypes.c_void_p), len(divisors), mism.data_ptr(),
+                                        first.data_ptr(), stream.cuda_stream)
+    assert rc == 0
+    assert int(mism.item()) == 0, f"first divisor with a difference: {int(first.item())}"
 
 
 @pytest.mark.parametrize("magnitude", [1e-6, 3e-3, 1.0, 250.0, 6.0e4])
