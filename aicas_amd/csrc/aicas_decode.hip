@@ -529,14 +529,27 @@ int aicas_kv_append(const aicas_kv_cache_t* cache, int32_t src_dtype, const void
   if (rc) return rc;
   if (cache->kv_dtype != AICAS_DTYPE_FP8_E4M3 && cache->kv_dtype != src_dtype)
     return fail(AICAS_ERR_UNSUPPORTED, "a 16-bit cache must have the dtype of the new rows");
+  // the kernel multiplies row indexes by 32-bit strides (the batch strides stay 64-bit)
+  const int64_t row_strides[] = {k_stride_h, k_stride_t, v_stride_h, v_stride_t, cache->stride_blk, cache->stride_h,
+                                 cache->stride_t, cache->k_scale ? cache->scale_stride_blk : 0,
+                                 cache->k_scale ? cache->scale_stride_h : 0};
+  for (const int64_t st : row_strides) {
+    if (st < 0 || st > int64_t{UINT32_MAX})
+      return fail(AICAS_ERR_UNSUPPORTED, "append strides must lie in [0, 2^32) elements (got %lld)", (long long)st);
+  }
   p.k_src = k_src;
   p.v_src = v_src;
   p.k_src_stride_b = k_stride_b;
-  p.k_src_stride_h = k_stride_h;
-  p.k_src_stride_t = k_stride_t;
   p.v_src_stride_b = v_stride_b;
-  p.v_src_stride_h = v_stride_h;
-  p.v_src_stride_t = v_stride_t;
+  p.src_stride_h[0] = static_cast<uint32_t>(k_stride_h);
+  p.src_stride_t[0] = static_cast<uint32_t>(k_stride_t);
+  p.src_stride_h[1] = static_cast<uint32_t>(v_stride_h);
+  p.src_stride_t[1] = static_cast<uint32_t>(v_stride_t);
+  p.dst_stride_blk = static_cast<uint32_t>(cache->stride_blk);
+  p.dst_stride_h = static_cast<uint32_t>(cache->stride_h);
+  p.dst_stride_t = static_cast<uint32_t>(cache->stride_t);
+  p.scale_stride_blk = static_cast<uint32_t>(cache->k_scale ? cache->scale_stride_blk : 0);
+  p.scale_stride_h = static_cast<uint32_t>(cache->k_scale ? cache->scale_stride_h : 0);
   p.positions = positions;
   p.seq_lens_out = seq_lens_out;
   p.status = status;

@@ -2,9 +2,9 @@
 //
 // aicas_calib_fp8_encoder_check: the fp8 encoding the kernels use (e4m3x4, gfx950's v_cvt_pk_fp8_f32) against
 // the encoder written out from the format (f32_to_e4m3) on every float with |x| <= 448;
-// aicas_calib_fp8_divide_check: the kernels' fp8 row quantiser (fp8_quantize: one reciprocal per row and a
-// corrected product per value) against the codes of the IEEE quotient, for every (row maximum, value) pair of
-// a 16-bit source type;
+// aicas_calib_fp8_divide_check: the kernels' fp8 row scale (fp8_scale_of), reciprocal (fp8_reciprocal) and
+// quantiser (fp8_quantize: one reciprocal per row and a corrected product per value) against the IEEE
+// divisions, for every row maximum and every (row maximum, value) pair of a 16-bit source type;
 // aicas_calib_fast_div_check: the launch-constant integer division (fast_div) against the division.
 // GPU tests require zero mismatches from each.
 //
@@ -106,15 +106,29 @@ __global__ __launch_bounds__(aicas::kBlockThreads) void fp8_encoder_check_kernel
 }
 
 // Block i takes the row maximum amax = the (i + 1)-th positive 16-bit pattern of DT (every one is finite for the
-// grid the host launches) and scale s = amax / 448, as fp8_row_scale gives it; thread t the 256 values with
-// patterns 256 t .. 256 t + 255, 4 at a time, those not finite or above amax in magnitude taken as 0.
+// grid the host launches); thread 0 compares the row scale (fp8_scale_of) with amax / 448 and, where the scale
+// takes the one-reciprocal path, fp8_reciprocal with 1 / s; thread t then compares the codes of the 256 values
+// with patterns 256 t .. 256 t + 255, 4 at a time (those not finite or above amax in magnitude taken as 0), with
+// those of the IEEE quotient. mismatches[0] counts code groups, [1] scales, [2] reciprocals.
 template <int DT>
 __global__ __launch_bounds__(aicas::kBlockThreads) void fp8_divide_check_kernel(unsigned long long* mismatches,
                                                                                uint32_t* first) {
   const uint32_t amax_bits = blockIdx.x + 1;
   float amax, unused;
   aicas::unpack2<DT>(amax_bits, amax, unused);
-  const float s = amax / 448.0f;
+  const float s_ref = amax / 448.0f;
+  const float s = aicas::fp8_scale_of(amax);
+  if (threadIdx.x == 0) {
+    if (__float_as_uint(s) != __float_as_uint(s_ref)) {
+      atomicAdd(mismatches + 1, 1ull);
+      atomicCAS(first, 0xffffffffu, amax_bits << 16);
+    }
+    if (s_ref >= aicas::kFp8FastDivMinScale &&
+        __float_as_uint(aicas::fp8_reciprocal(s_ref)) != __float_as_uint(1.0f / s_ref)) {
+      atomicAdd(mismatches + 2, 1ull);
+      atomicCAS(first, 0xffffffffu, amax_bits << 16);
+    }
+  }
   unsigned long long bad = 0;
   for (int g = 0; g < 64; ++g) {
     const uint32_t base = threadIdx.x * 256u + 4u * g;
@@ -124,7 +138,7 @@ __global__ __launch_bounds__(aicas::kBlockThreads) void fp8_divide_check_kernel(
       float v;
       aicas::unpack2<DT>(base + j, v, unused);
       x[j] = fabsf(v) <= amax ? v : 0.0f;
-      y[j] = fminf(fmaxf(x[j] / s, -448.0f), 448.0f);
+      y[j] = fminf(fmaxf(x[j] / s_ref, -448.0f), 448.0f);
     }
     uint32_t codes;
     aicas::fp8_quantize<4>(x, s, &codes);
@@ -191,14 +205,14 @@ int aicas_calib_fp8_encoder_check(unsigned long long* mismatches, uint32_t* firs
   return hipStreamSynchronize(stream) == hipSuccess ? 0 : 2;
 }
 
-// src_dtype 0 (bf16) or 1 (fp16): every positive finite row maximum and every value of that type through
-// fp8_quantize and through the IEEE quotient's codes; *mismatches (zeroed here) counts the groups of 4 values
-// whose codes differ, *first_pattern (0xffffffff here) holds (amax pattern << 16 | value pattern) of the first.
-// Synchronous.
+// src_dtype 0 (bf16) or 1 (fp16): every positive finite row maximum and every value of that type through the
+// kernels' row scale, reciprocal and quantiser, against the IEEE divisions; mismatches[3] (zeroed here): groups
+// of 4 values whose codes differ, scales that differ, reciprocals that differ; *first_pattern (0xffffffff here)
+// holds (amax pattern << 16 | value pattern) of the first difference. Synchronous.
 int aicas_calib_fp8_divide_check(int32_t src_dtype, unsigned long long* mismatches, uint32_t* first_pattern,
                                  hipStream_t stream) {
   if (!mismatches || !first_pattern || (src_dtype != aicas::kBF16 && src_dtype != aicas::kFP16)) return 1;
-  if (hipMemsetAsync(mismatches, 0, sizeof(unsigned long long), stream) != hipSuccess) return 2;
+  if (hipMemsetAsync(mismatches, 0, 3 * sizeof(unsigned long long), stream) != hipSuccess) return 2;
   if (hipMemsetAsync(first_pattern, 0xff, sizeof(uint32_t), stream) != hipSuccess) return 2;
   // positive finite patterns: bf16 0x0001 .. 0x7f7f, fp16 0x0001 .. 0x7bff
   if (src_dtype == aicas::kBF16)

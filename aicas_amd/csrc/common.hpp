@@ -153,40 +153,59 @@ __device__ __forceinline__ float group_sum(float x) {
 }
 
 template <int N>
-__device__ __forceinline__ float group_max(float x) {
-  if constexpr (N >= 2) x = fmaxf(x, dpp_f32<0xB1>(x));
-  if constexpr (N >= 4) x = fmaxf(x, dpp_f32<0x4E>(x));
-  if constexpr (N >= 8) x = fmaxf(x, dpp_f32<0x141>(x));
-  if constexpr (N >= 16) x = fmaxf(x, dpp_f32<0x140>(x));
+__device__ __forceinline__ uint32_t group_max_u32(uint32_t x) {
+  if constexpr (N >= 2) x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0xB1, 0xF, 0xF, false)));
+  if constexpr (N >= 4) x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x4E, 0xF, 0xF, false)));
+  if constexpr (N >= 8) x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x141, 0xF, 0xF, false)));
+  if constexpr (N >= 16) x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x140, 0xF, 0xF, false)));
   return x;
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// amax / 448 correctly rounded: for amax >= 2^-100 from the constant y = 1 / 448 (correctly rounded at compile
+// time), q0 = amax * y and one correction q0 + (amax - 448 q0) y (Markstein's theorem, the residual exact in an
+// FMA); below that by the IEEE division. aicas_calib_fp8_divide_check compares it with the division for every
+// 16-bit row maximum.
+__device__ __forceinline__ float fp8_scale_of(float amax) {
+  constexpr float kInv448 = 1.0f / 448.0f;
+  if (amax >= 0x1p-100f) {
+    const float q0 = amax * kInv448;
+    return fmaf(fmaf(-q0, 448.0f, amax), kInv448, q0);
+  }
+  return amax / 448.0f;
+}
+
 // Scale of one fp8 cache row spread over N aligned lanes (VEC values each; every lane of the row takes part):
 // amax / 448, 0 for an all-zero row. A row holding any NaN or +-Inf gets a NaN scale (and, from the caller's
 // `scale > 0` test, all-zero codes), so that it dequantises to NaN everywhere, as the unquantised row would make
-// every score that touches it non-finite; `nonfinite` reports it.
+// every score that touches it non-finite; `nonfinite` reports it. The maximum is taken over the magnitudes' bit
+// patterns, which order like the magnitudes, with Inf and every NaN above all finite values: one reduction
+// finds both.
 template <int N, int VEC>
 __device__ __forceinline__ float fp8_row_scale(const float* f, bool& nonfinite) {
-  float amax = 0.0f, bad = 0.0f;
+  uint32_t m = 0;
 #pragma unroll
-  for (int i = 0; i < VEC; ++i) {
-    const float a = fabsf(f[i]);
-    amax = fmaxf(amax, a);
-    bad = a <= 3.402823466e38f ? bad : 1.0f;  // false for NaN and Inf
-  }
-  amax = group_max<N>(amax);
-  nonfinite = group_max<N>(bad) > 0.0f;
-  return nonfinite ? __builtin_nanf("") : amax / 448.0f;
+  for (int i = 0; i < VEC; ++i) m = max(m, __float_as_uint(f[i]) & 0x7fffffffu);
+  m = group_max_u32<N>(m);
+  nonfinite = m >= 0x7f800000u;
+  return nonfinite ? __builtin_nanf("") : fp8_scale_of(__uint_as_float(m));
 }
 
 // Row scales at or above this take the one-reciprocal division in fp8_quantize.
 constexpr float kFp8FastDivMinScale = 0x1p-90f;
 
+// 1 / s for a row scale s >= kFp8FastDivMinScale: the hardware reciprocal (v_rcp_f32) and one Newton step. It is
+// the correctly rounded reciprocal for every scale a 16-bit row maximum gives (fp8_scale_of of every positive
+// bf16 and fp16 value), which aicas_calib_fp8_divide_check compares with 1.0f / s.
+__device__ __forceinline__ float fp8_reciprocal(float s) {
+  const float r0 = __builtin_amdgcn_rcpf(s);
+  return fmaf(fmaf(-s, r0, 1.0f), r0, r0);
+}
+
 // The e4m3 codes of VEC finite values of one fp8 cache row with scale s (fp8_row_scale): clamp(x / s, +-448)
 // encoded by e4m3x4, code i in byte i % 4 of packed[i / 4]; a zero or poisoned row (s not > 0) gets zero codes.
-// The quotient is x / s correctly rounded, from one division per row: y = 1 / s (IEEE), then per value
+// The quotient is x / s correctly rounded, from one reciprocal per row: y = 1 / s (fp8_reciprocal), then per value
 // q0 = x * y and one correction q = q0 + (x - s q0) y with the residual exact in an FMA — Markstein's theorem
 // (y the correctly rounded reciprocal and q0 within an ulp of x / s make q the correctly rounded quotient) —
 // provided the residual does not underflow; the sign is then x's (the correction would give +0 for -0). For
@@ -198,7 +217,7 @@ template <int VEC>
 __device__ __forceinline__ void fp8_quantize(const float* f, float s, uint32_t* packed) {
   float y[VEC];
   if (s >= kFp8FastDivMinScale) {
-    const float r = 1.0f / s;
+    const float r = fp8_reciprocal(s);
 #pragma unroll
     for (int i = 0; i < VEC; ++i) {
       const float q0 = f[i] * r;

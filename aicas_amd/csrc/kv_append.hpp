@@ -24,8 +24,12 @@ struct AppendParams {
   KVLayout cache;
   const void* k_src;
   const void* v_src;
-  int64_t k_src_stride_b, k_src_stride_h, k_src_stride_t;  // elements; the head_dim stride is 1
-  int64_t v_src_stride_b, v_src_stride_h, v_src_stride_t;
+  int64_t k_src_stride_b, v_src_stride_b;  // elements; the head_dim stride is 1
+  // The per-row strides as 32-bit values (the host checks that they fit), so that each term of a row's offset is
+  // one 32 x 32 -> 64-bit multiply-add: [0] K, [1] V.
+  uint32_t src_stride_h[2], src_stride_t[2];
+  uint32_t dst_stride_blk, dst_stride_h, dst_stride_t;  // cache rows (elements)
+  uint32_t scale_stride_blk, scale_stride_h;            // fp8 scales (token stride 1)
   const int32_t* positions;
   int32_t* seq_lens_out;
   int32_t* status;
@@ -48,7 +52,6 @@ __global__ __launch_bounds__(kBlockThreads) void kv_append_kernel(AppendParams p
   static_assert(R >= 1 && R <= 16, "a row must fit one DPP row");
   constexpr int ROWS_PER_PASS = kBlockThreads / R;
 
-  __shared__ int32_t s_pos;
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
   const int lane = tid % R;
@@ -65,32 +68,32 @@ __global__ __launch_bounds__(kBlockThreads) void kv_append_kernel(AppendParams p
     h = fast_div(rr, p.div_n_new);
     j = rr - h * p.n_new;
   };
-  auto src_row = [&](int r) -> const uint16_t* {
-    int which, h, j;
-    row_coords(r, which, h, j);
-    return which == 0 ? static_cast<const uint16_t*>(p.k_src) + b * p.k_src_stride_b + h * p.k_src_stride_h +
-                            j * p.k_src_stride_t
-                      : static_cast<const uint16_t*>(p.v_src) + b * p.v_src_stride_b + h * p.v_src_stride_h +
-                            j * p.v_src_stride_t;
-  };
-  // Every pass's rows are loaded before the position is known, overlapping the reads.
+  const uint16_t* const k_src_b = static_cast<const uint16_t*>(p.k_src) + b * p.k_src_stride_b;
+  const uint16_t* const v_src_b = static_cast<const uint16_t*>(p.v_src) + b * p.v_src_stride_b;
+  // Every pass's rows are loaded before the position is known, overlapping the reads; rows past the last (a
+  // partial last workgroup) load the last row again, unused, so that every load is issued unconditionally.
   uint4 x[kAppendPasses];
 #pragma unroll
   for (int k = 0; k < kAppendPasses; ++k) {
-    const int r = first_row + k * ROWS_PER_PASS;
-    x[k] = r < rows_total ? load_stream16(src_row(r) + lane * VEC) : make_uint4(0u, 0u, 0u, 0u);
+    int which, h, j;
+    row_coords(min(first_row + k * ROWS_PER_PASS, rows_total - 1), which, h, j);
+    // selects between values held in scalar registers (indexing the argument arrays by `which` would load the
+    // chosen field per lane)
+    const uint32_t sh = which == 0 ? p.src_stride_h[0] : p.src_stride_h[1];
+    const uint32_t st = which == 0 ? p.src_stride_t[0] : p.src_stride_t[1];
+    const uint16_t* src = (which == 0 ? k_src_b : v_src_b) + (static_cast<uint64_t>(static_cast<uint32_t>(h)) * sh +
+                                                              static_cast<uint64_t>(static_cast<uint32_t>(j)) * st);
+    x[k] = load_stream16(src + lane * VEC);
   }
-  if (tid == 0) s_pos = p.positions[b];
-  __syncthreads();
-  const int pos = s_pos;
+  const int pos = p.positions[b];  // uniform: every wave reads it
 
   // Where every pass's row goes. Paged caches: the block ids of all passes are loaded together (each index
   // clamped into the table), then checked, so that the passes do not wait for them one after another.
-  int64_t dst_row[kAppendPasses], dst_srow[kAppendPasses];
+  uint64_t dst_row[kAppendPasses], dst_srow[kAppendPasses];
   bool dst_ok[kAppendPasses];
   {
     int tok[kAppendPasses], head[kAppendPasses];
-    int64_t blk[kAppendPasses];
+    int32_t blk[kAppendPasses];
 #pragma unroll
     for (int k = 0; k < kAppendPasses; ++k) {
       int which, j;
@@ -110,7 +113,6 @@ __global__ __launch_bounds__(kBlockThreads) void kv_append_kernel(AppendParams p
 #pragma unroll
     for (int k = 0; k < kAppendPasses; ++k) {
       const int r = first_row + k * ROWS_PER_PASS;
-      const int h = head[k];
       const int t = tok[k];
       const bool live = r < rows_total;
       const bool in_cache = t >= 0 && t < p.cache.max_tokens;
@@ -118,9 +120,12 @@ __global__ __launch_bounds__(kBlockThreads) void kv_append_kernel(AppendParams p
       if (live && !in_cache) flags |= kStatusAppendOverflow;
       else if (live && !valid) flags |= kStatusBlockOutOfRange;
       dst_ok[k] = live && in_cache && valid;
-      const int tin = p.cache.block_table ? t & page_mask : t;
-      dst_row[k] = blk[k] * p.cache.stride_blk + h * p.cache.stride_h + static_cast<int64_t>(tin) * p.cache.stride_t;
-      dst_srow[k] = blk[k] * p.cache.scale_stride_blk + h * p.cache.scale_stride_h + tin;
+      const uint32_t ublk = static_cast<uint32_t>(blk[k]), uh = static_cast<uint32_t>(head[k]);
+      const uint32_t tin = static_cast<uint32_t>(p.cache.block_table ? t & page_mask : t);
+      dst_row[k] = static_cast<uint64_t>(ublk) * p.dst_stride_blk + static_cast<uint64_t>(uh) * p.dst_stride_h +
+                   static_cast<uint64_t>(tin) * p.dst_stride_t;
+      dst_srow[k] = static_cast<uint64_t>(ublk) * p.scale_stride_blk + static_cast<uint64_t>(uh) * p.scale_stride_h +
+                    tin;
     }
     if (flags && p.status && lane == 0) atomicOr(p.status, flags);
   }
@@ -135,7 +140,7 @@ __global__ __launch_bounds__(kBlockThreads) void kv_append_kernel(AppendParams p
     const int r = first_row + k * ROWS_PER_PASS;
     if (r >= rows_total) continue;  // the whole row group (R lanes) skips together
     const int which = r >= rows_per_tensor ? 1 : 0;
-    const int64_t row = dst_row[k], srow = dst_srow[k];
+    const uint64_t row = dst_row[k], srow = dst_srow[k];
     const bool ok = dst_ok[k];
     if constexpr (KV_DT == kFP8E4M3) {
       float f[VEC];
@@ -162,7 +167,7 @@ __global__ __launch_bounds__(kBlockThreads) void kv_append_kernel(AppendParams p
     }
   }
   if (gridDim.x == 1) {
-    __syncthreads();
+    __syncthreads();  // every wave has read positions[b] (which seq_lens_out may alias)
     if (tid == 0 && p.seq_lens_out) p.seq_lens_out[b] = pos + p.n_new;
   }
 }

@@ -2,9 +2,10 @@
 
 The kernels quantise with gfx950's fp8 conversion instruction (e4m3x4). Exhaustively, on every float with
 |x| <= 448 (the clamped domain the kernels feed it), it must give the codes of the encoder written out from the
-OCP e4m3 format (round to nearest even). The quotient x / scale comes from one reciprocal per row and a
-corrected product per value (fp8_quantize); for every (row maximum, value) pair of bf16 and of fp16 sources its
-codes must be those of the IEEE quotient. On rows of every magnitude, through the product's own append, codes and
+OCP e4m3 format (round to nearest even). The row scale amax / 448 comes from a corrected product, and the
+quotient x / scale from one reciprocal per row (hardware reciprocal and a Newton step) and a corrected product per
+value (fp8_quantize); for every row maximum of bf16 and of fp16 sources the scale and the reciprocal must be the
+IEEE quotients' bits, and for every (row maximum, value) pair the codes those of the IEEE quotient. On rows of every magnitude, through the product's own append, codes and
 scales must be the oracle's (torch's cast of clamp(x / scale)). The append kernel divides row indexes by the
 launch's new-row count with a multiplier (fast_div); on 2^25 dividends spread over the 31-bit range it must
 equal the division for every divisor tried.
@@ -37,12 +38,15 @@ def test_hardware_encoder_matches_format_encoder_on_every_float(dev):
 def test_row_quantiser_gives_the_ieee_quotient_codes(dev, src_dtype, name):
     lib = ctypes.CDLL(CALIB_OUTPUT, mode=ctypes.RTLD_LOCAL)
     lib.aicas_calib_fp8_divide_check.argtypes = [ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
-    mism = torch.zeros(1, dtype=torch.int64, device=dev)
+    mism = torch.zeros(3, dtype=torch.int64, device=dev)
     first = torch.zeros(1, dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream(dev)
     assert lib.aicas_calib_fp8_divide_check(src_dtype, mism.data_ptr(), first.data_ptr(), stream.cuda_stream) == 0
     f = int(first.item()) & 0xffffffff
-    assert int(mism.item()) == 0, f"{name}: row maximum {f >> 16:#06x}, values from {f & 0xffff:#06x}"
+    codes, scales, recips = mism.cpu().tolist()
+    assert (codes, scales, recips) == (0, 0, 0), \
+        f"{name}: {codes} code groups, {scales} scales, {recips} reciprocals differ; first at row maximum " \
+        f"{f >> 16:#06x}, values from {f & 0xffff:#06x}"
 
 
 def test_launch_constant_division(dev):
