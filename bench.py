@@ -659,6 +659,15 @@ def prefill(args) -> int:
             for v in views:
                 ops.kv_append(v, k_src, v_src, pos)
             torch.cuda.synchronize()
+            if args.mode == "eager":  # every dispatch its own (for counter runs)
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(reps):
+                    for v in views:
+                        ops.kv_append(v, k_src, v_src, pos)
+                e1.record()
+                torch.cuda.synchronize()
+                return e0.elapsed_time(e1) * 1e3 / (reps * len(views))
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph, stream=stream):
                 for v in views:
@@ -677,6 +686,14 @@ def prefill(args) -> int:
     rows = 2 * B * HKV * N
     fp8_bytes = rows * D * 2 + rows * (D + 4)
     bf16_bytes = rows * D * 2 * 2
+    if args.copy_calibration_mib > 0:  # a device copy of known size beside the kernel, for counter runs
+        n = args.copy_calibration_mib << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).random_(0, 255)
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     us_fp8 = per_launch_us(paged)
     us_bf16 = per_launch_us(dense)
 
