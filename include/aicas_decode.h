@@ -94,10 +94,13 @@ typedef struct aicas_kv_cache {
  * e4m3(clamp(x / s, -448, 448)) with s = max|row| / 448 stored in k_scale / v_scale (s = 0 and all-zero
  * codes for an all-zero row; a row holding any NaN or +-Inf is stored poisoned, s = NaN and all-zero codes, so
  * that it dequantises to NaN, and AICAS_STATUS_NONFINITE_ROW is set). If seq_lens_out is not NULL,
- * seq_lens_out[b] = positions[b] + n_new is written after the rows; it may alias positions. A row whose position falls outside the cache is dropped
- * and AICAS_STATUS_APPEND_OVERFLOW is ORed into *status (status may be NULL). batch <= 65535. A decode step's
- * append is one launch; a prefill-sized one (a prompt written into the cache) spreads each sequence's rows
- * over many workgroups and bumps the lengths in a second, one-thread-per-sequence launch.
+ * seq_lens_out[b] = positions[b] + n_new is written after the rows; it may alias positions. A row whose
+ * position falls outside the cache is dropped and AICAS_STATUS_APPEND_OVERFLOW is ORed into *status (status may
+ * be NULL). batch <= 65535 and 2 * num_kv_heads * n_new < 2^31; the head and token strides of k_src / v_src and
+ * the cache's stride_blk, stride_h, stride_t and scale strides must lie in [0, 2^32) elements (the batch strides
+ * of k_src / v_src are unrestricted); otherwise AICAS_ERR_UNSUPPORTED. A decode step's append is one launch; a
+ * prefill-sized one (a prompt written into the cache) spreads each sequence's rows over many workgroups and
+ * bumps the lengths in a second, one-thread-per-sequence launch.
  * Replaces: transformers/cache_utils.py:127-146; dujunbaoV1/evaluation_wrapper.py:84-100, :162-175;
  * new KV cache/evaluation_wrapper.py:143-195.
  */

@@ -214,6 +214,9 @@ def test_append_argument_errors():
     assert call(src=_lib.DTYPE_FP16) == _lib.ERR_UNSUPPORTED and "dtype of the new rows" in _last_error()
     assert call(kh=100) == _lib.ERR_INVALID
     assert call(D=48) == _lib.ERR_UNSUPPORTED
+    # the kernel's row strides are 32-bit, its row indexes 31-bit
+    assert call(kh=1 << 32) == _lib.ERR_UNSUPPORTED and "[0, 2^32)" in _last_error()
+    assert call(n=1 << 27, H=8) == _lib.ERR_UNSUPPORTED and "too many rows" in _last_error()
 
 
 @no_gpu_only
