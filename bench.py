@@ -624,6 +624,18 @@ def gather(args) -> int:
     return 0 if max_err == 0 else 1
 
 
+def prefill_bytes(batch: int, kv_heads: int, n_new: int, head_dim: int, fp8: bool = False, page: int = 0) -> int:
+    """Algorithmic bytes of one aicas_kv_append launch writing n_new tokens per sequence from position 0: the
+    16-bit source rows read (K and V), the cache rows written (fp8: one code byte per element and a 4-byte scale
+    per row; 16-bit: the rows as they are), the block-table entries of the pages written (paged caches) and the
+    positions read."""
+    rows = 2 * batch * kv_heads * n_new
+    src = rows * head_dim * 2
+    dst = rows * (head_dim + 4) if fp8 else rows * head_dim * 2
+    table = batch * -(-n_new // page) * 4 if page else 0
+    return src + dst + table + batch * 4
+
+
 def prefill(args) -> int:
     """--config prefill: the prefill writer, one aicas_kv_append launch that writes a 2048-token prompt for each
     of 32 sequences (8 kv heads, head_dim 128) into the C5 layout (16-token pages over a permuted block table,
@@ -683,9 +695,8 @@ def prefill(args) -> int:
             torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e3 / (reps * len(views))
 
-    rows = 2 * B * HKV * N
-    fp8_bytes = rows * D * 2 + rows * (D + 4)
-    bf16_bytes = rows * D * 2 * 2
+    fp8_bytes = prefill_bytes(B, HKV, N, D, fp8=True, page=PAGE)
+    bf16_bytes = prefill_bytes(B, HKV, N, D)
     if args.copy_calibration_mib > 0:  # a device copy of known size beside the kernel, for counter runs
         n = args.copy_calibration_mib << 20
         src = torch.empty(n, dtype=torch.uint8, device=dev).random_(0, 255)

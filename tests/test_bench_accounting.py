@@ -2,7 +2,7 @@
 
 The algorithmic bytes per layer-step are what the roofline fraction divides by, so they are pinned here by
 hand-counted cases: B=8 L=2048 with 64.5 decode steps on average (the headline's mean length after the
-append, 2112.5 tokens), and a small paged fp8 case counted term by term.
+append, 2112.5 tokens), a small paged fp8 case counted term by term, and the prefill writer's launch.
 """
 
 import os
@@ -33,6 +33,17 @@ def test_paged_fp8_bytes_term_by_term():
     table = (2 + 3) * 4 + 2 * 4                  # block-table entries of 2 and 3 pages, and the lengths
     got = bench.algorithmic_bytes(2, 4, 2, 128, lens, fp8=True, page=page)
     assert got == kv + new_rows + q_out + table
+
+
+def test_prefill_bytes_term_by_term():
+    # 2 sequences x 3 kv heads x 40 new tokens, head_dim 64, from position 0
+    rows = 2 * 2 * 3 * 40                        # K and V rows
+    src = rows * 64 * 2                          # bf16 rows read
+    assert bench.prefill_bytes(2, 3, 40, 64) == src + rows * 64 * 2 + 2 * 4
+    # paged fp8 with 16-token pages: 3 pages per sequence written, one table entry each
+    assert bench.prefill_bytes(2, 3, 40, 64, fp8=True, page=16) == src + rows * (64 + 4) + 2 * 3 * 4 + 2 * 4
+    # the bench's prefill line: 32 sequences, 8 kv heads, a 2048-token prompt, 16-token pages
+    assert bench.prefill_bytes(32, 8, 2048, 128, fp8=True, page=16) == 268_435_456 + 138_412_032 + 16_384 + 128
 
 
 def test_more_than_one_gpu_is_refused_before_any_gpu_work():
