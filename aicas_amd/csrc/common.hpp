@@ -208,9 +208,9 @@ __device__ __forceinline__ float fp8_reciprocal(float s) {
 // The quotient is x / s correctly rounded, from one reciprocal per row: y = 1 / s (fp8_reciprocal), then per value
 // q0 = x * y and one correction q = q0 + (x - s q0) y with the residual exact in an FMA — Markstein's theorem
 // (y the correctly rounded reciprocal and q0 within an ulp of x / s make q the correctly rounded quotient) —
-// provided the residual does not underflow; the sign is then x's (the correction would give +0 for -0). For
-// s >= 2^-90 that holds whenever |x / s| >= 2^-11, and smaller quotients encode to a zero of x's sign whatever
-// their last bits; smaller scales divide value by value. So the codes are
+// provided the residual does not underflow. For s >= 2^-90 that holds whenever |x / s| >= 2^-11, and smaller
+// quotients encode to a zero of x's sign whatever their last bits; smaller scales divide value by value (and
+// clamp: a subnormal s can be far from amax / 448). So the codes are
 // those of the IEEE quotient for every input, which libaicas_calib.so's aicas_calib_fp8_divide_check compares
 // over every (row maximum, value) pair of both 16-bit source types.
 template <int VEC>
@@ -218,12 +218,13 @@ __device__ __forceinline__ void fp8_quantize(const float* f, float s, uint32_t* 
   float y[VEC];
   if (s >= kFp8FastDivMinScale) {
     const float r = fp8_reciprocal(s);
+    // The residual enters negated, q = q0 - (q0 s - x) r: the same rounded value as q0 + (x - q0 s) r for every
+    // nonzero quotient, and a zero quotient keeps x's sign (the other order turns -0 into +0). No clamp: with s
+    // a normal number |x / s| <= 448 (1 + 2^-23) < 464, which e4m3 rounds to at most 448.
 #pragma unroll
     for (int i = 0; i < VEC; ++i) {
       const float q0 = f[i] * r;
-      // the correction's sum turns a -0 quotient into +0: the quotient has the sign of x (s > 0)
-      const float q = copysignf(fmaf(fmaf(-q0, s, f[i]), r, q0), f[i]);
-      y[i] = fminf(fmaxf(q, -448.0f), 448.0f);
+      y[i] = fmaf(-fmaf(q0, s, -f[i]), r, q0);
     }
   } else if (s > 0.0f) {
 #pragma unroll

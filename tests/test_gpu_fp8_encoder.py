@@ -1,8 +1,9 @@
 """The fp8 encoding of the append kernels, and the launch-constant integer division of the append kernel.
 
 The kernels quantise with gfx950's fp8 conversion instruction (e4m3x4). Exhaustively, on every float with
-|x| <= 448 (the clamped domain the kernels feed it), it must give the codes of the encoder written out from the
-OCP e4m3 format (round to nearest even). The row scale amax / 448 comes from a corrected product, and the
+|x| <= 448, it must give the codes of the encoder written out from the OCP e4m3 format (round to nearest even);
+the quotients a hair above 448 that the kernels also feed it (|x / s| <= 448 (1 + 2^-23) for a normal scale) are
+covered by the row quantiser's check, which compares with the codes of the clamped IEEE quotient. The row scale amax / 448 comes from a corrected product, and the
 quotient x / scale from one reciprocal per row (hardware reciprocal and a Newton step) and a corrected product per
 value (fp8_quantize); for every row maximum of bf16 and of fp16 sources the scale and the reciprocal must be the
 IEEE quotients' bits, and for every (row maximum, value) pair the codes those of the IEEE quotient. On rows of every magnitude, through the product's own append, codes and
