@@ -220,6 +220,7 @@ struct Plan {
   int32_t tokens_per_split;  // a sequence of L tokens takes min(num_splits, ceil(L / tokens_per_split)) splits
   int32_t num_splits;
   int32_t len_limit;  // longest sequence the launch can attend in full (paged caches: LDS block-id cache)
+  bool many_pairs;    // more (batch row, kv head) pairs than 3/4 of the compute units: a ragged batch's shape
   size_t ml_off, acc_off, bytes;
 };
 
@@ -239,6 +240,10 @@ int plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int32_t num_kv_he
   // kMaxBlockEntries block-table entries: at most `cap` tokens per split.
   const int64_t cap = page_size > 0 ? (int64_t{aicas::kMaxBlockEntries} - 2) * page_size / tpi * tpi : 0;
   int64_t tps, splits;
+  const int64_t pairs = int64_t{batch} * num_kv_heads;
+  const int64_t cus = device_cus();
+  const bool few = pairs * 4 <= 3 * cus;  // at most 3/4 of a pair per CU
+  pl.many_pairs = !few;
   if (hint > 0) {
     tps = ceil_div(hint, rpb) * rpb;
     if (cap >= tpi && tps > cap) tps = cap;
@@ -247,9 +252,6 @@ int plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int32_t num_kv_he
     // Split count: the workgroups per compute unit above, in total. A split covers at least one super-chunk
     // (two chunks) per wave: below that its merge costs more than its streaming saves (B=1 L=1024: 17 splits
     // 9.19 us, 9 splits 8.02 us).
-    const int64_t pairs = int64_t{batch} * num_kv_heads;
-    const int64_t cus = device_cus();
-    const bool few = pairs * 4 <= 3 * cus;  // at most 3/4 of a pair per CU
     const int64_t target = int64_t{few ? kFewPairsWGsPerCUx8 : kManyPairsWGsPerCUx8} * cus / 8;
     int64_t splits_wanted = std::max<int64_t>(1, (target + pairs / 2) / pairs);
     if (few) {
@@ -359,6 +361,11 @@ int run_decode(const DecodeCall& c, hipStream_t stream) {
   // Every workgroup of a batch row counts itself in on that row's counter; counters sharing a cache line
   // serialise each other's atomics, so each row gets a 128-byte line of its own while the region allows.
   p.arrive_stride = static_cast<int32_t>(std::min<int64_t>(32, kMaxPairs / c.batch));
+  // Ragged batches (many pairs, device lengths): rows dispatched longest first, so that rows of similar length
+  // run together. Measured on MI355X with the rows sorted on the host: B=32 paged fp8 U{256..8192} 74.7 -> 70.5
+  // us per launch, B=64 bf16 U{512..4096} 28 layers 3172 -> 3030 us per step. The kernel ranks the rows itself,
+  // one thread per row.
+  p.order_rows = (pl.many_pairs && c.lens && c.batch > 1 && c.batch <= aicas::kBlockThreads) ? 1 : 0;
   p.ws_ml = reinterpret_cast<float*>(ws + pl.ml_off);
   p.ws_acc = reinterpret_cast<float*>(ws + pl.acc_off);
   p.status = c.status;

@@ -46,7 +46,8 @@
 // attention then using the dequantised row, exactly what a separate append followed by attention would read).
 // Every workgroup of batch row b counts itself in on its way out, once all its waves have read positions[b];
 // the last one to do so stores positions[b] + 1 to seq_lens_out[b] (which may alias positions), so no workgroup
-// can read a bumped length.
+// can read a bumped length. With the rows in length order (order_rows), where every workgroup reads every row's
+// length, the count covers the whole launch and its last workgroup bumps every row.
 #pragma once
 
 #include <type_traits>
@@ -76,6 +77,8 @@ struct DecodeParams {
   int32_t* ws_counter; // [B * Hkv] split arrivals, zero between launches
   int32_t* ws_arrive;  // [B * arrive_stride] APPEND: readers of positions[b], zero between launches
   int32_t arrive_stride;  // int32 slots between batch rows' counters (32: one 128-byte line each)
+  int32_t order_rows;     // nonzero: grid slot z takes the batch row of rank z by length (longest first); needs
+                          // seq_lens and B <= kBlockThreads
   int32_t* status;
   // APPEND only
   const void* k_new;
@@ -207,6 +210,10 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   auto& s_acc = *reinterpret_cast<float (*)[kWavesPerBlock][G][D]>(s_pool);
   __shared__ int32_t s_bt[PAGED ? kMaxBlockEntries : 1];
   __shared__ int32_t s_last;
+  // order_rows: every batch row's length as read at the start (APPEND: before any bump), and this slot's row
+  __shared__ int32_t s_row_len[kBlockThreads];
+  __shared__ int32_t s_row;
+  __shared__ int32_t s_bump;
   // APPEND: the new token's rows as the attention must see them (dequantised codes for fp8 caches)
   __shared__ uint4 s_new[APPEND ? 2 * R : 1];
   __shared__ float s_new_scale[APPEND && FP8 ? 2 : 1];
@@ -215,8 +222,28 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
 
   const int split = blockIdx.x;
   const int kvh = blockIdx.y;
-  const int b = blockIdx.z;
   const int tid = threadIdx.x;
+  // Row order (ragged batches): grid slot z takes the batch row of rank z in decreasing length (ties in row order),
+  // so that rows of similar length are dispatched together. Every workgroup reads all the lengths and ranks them
+  // the same way (none is bumped before every workgroup has counted in, see count_in), so the slots cover every
+  // row exactly once.
+  int b = blockIdx.z;
+  if (p.order_rows) {
+    const int nb = gridDim.z;
+    const int len_t = tid < nb ? p.seq_lens[tid] : 0;
+    s_row_len[tid] = len_t;
+    __syncthreads();
+    if (tid < nb) {
+      int rank = 0;
+      for (int j = 0; j < nb; ++j) {
+        const int len_j = s_row_len[j];
+        rank += (len_j > len_t || (len_j == len_t && j < tid)) ? 1 : 0;
+      }
+      if (rank == static_cast<int>(blockIdx.z)) s_row = tid;
+    }
+    __syncthreads();
+    b = __builtin_amdgcn_readfirstlane(s_row);
+  }
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // uniform across the wave: scalar control flow
   const int lane = tid % kWave;
   const int row = lane / R;
@@ -377,6 +404,21 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   // contended atomic off the start of the stream.
   auto count_in = [&]() {
     if constexpr (APPEND) {
+      if (p.order_rows) {
+        // every workgroup has read every row's length: the last of the whole launch bumps them all (from the
+        // values read at the start, as the per-row counters below would)
+        if (p.seq_lens_out) {
+          if (tid == 0) {
+            const int readers = gridDim.x * gridDim.y * gridDim.z;
+            const int prev = __hip_atomic_fetch_add(p.ws_arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_bump = prev == readers - 1 ? 1 : 0;
+            if (prev == readers - 1) __hip_atomic_store(p.ws_arrive, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+          __syncthreads();
+          if (s_bump && tid < static_cast<int>(gridDim.z)) p.seq_lens_out[tid] = s_row_len[tid] + 1;
+        }
+        return;
+      }
       if (tid == 0 && p.seq_lens_out) {
         const int readers = gridDim.x * gridDim.y;
         int32_t* const arrive = p.ws_arrive + static_cast<int64_t>(b) * p.arrive_stride;

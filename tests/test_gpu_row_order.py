@@ -1,0 +1,121 @@
+"""Ragged batches with many (batch row, kv head) pairs are dispatched longest first.
+
+When a launch has more pairs than 3/4 of the compute units, device lengths and at most 256 batch rows, every
+workgroup reads all the rows' lengths, ranks them (decreasing length, ties in row order) and takes the row whose
+rank is its grid slot; the fused append's length bump then waits for every workgroup of the launch, not only
+those of the row. The order may change the timing only: the fused launch must still equal the append followed
+by the plain decode bit for bit, cover every row (ties and empty sequences included), bump every length by one,
+leave the workspace counters at zero and match the oracle. 257 rows take the natural order.
+"""
+
+import math
+
+import pytest
+import torch
+
+from aicas_amd import ops
+from oracle import reference_path as ref
+
+pytestmark = pytest.mark.gpu
+
+H, G, D = 8, 2, 128
+COUNTER_BYTES = 512 << 10  # the workspace's counters, ahead of the split partials
+
+
+def _caches(dev, gen, kind, B, cap):
+    """Two identical caches (fused / two-launch copies) holding random rows."""
+    if kind == "bf16":
+        k = torch.randn((B, H, cap, D), generator=gen).to(torch.bfloat16)
+        v = torch.randn((B, H, cap, D), generator=gen).to(torch.bfloat16)
+        return [ops.KVCacheView(k.clone().to(dev), v.clone().to(dev)) for _ in range(2)]
+    page = 16
+    per_seq = math.ceil(cap / page)
+    nblocks = B * per_seq + 3
+    bt = torch.randperm(nblocks, generator=gen)[: B * per_seq].to(torch.int32).view(B, per_seq)
+    ck, sk = ref.fp8_quantize_rows(torch.randn((nblocks, H, page, D), generator=gen).to(torch.bfloat16))
+    cv, sv = ref.fp8_quantize_rows(torch.randn((nblocks, H, page, D), generator=gen).to(torch.bfloat16))
+    return [ops.KVCacheView(ck.clone().to(dev), cv.clone().to(dev), sk.clone().to(dev), sv.clone().to(dev),
+                            bt.to(dev)) for _ in range(2)]
+
+
+@pytest.mark.parametrize("B, kind", [(40, "bf16"), (40, "fp8_paged"), (256, "bf16"), (257, "bf16")])
+def test_ordered_rows_fused_equals_two_launches_and_oracle(dev, status, B, kind):
+    gen = torch.Generator().manual_seed(900 + B + (1 if kind != "bf16" else 0))
+    cap = 640
+    lens = torch.randint(0, 600, (B,), generator=gen).tolist()
+    lens[0] = 0
+    for i in range(3, B, 7):  # ties: equal lengths rank in row order
+        lens[i] = lens[1]
+    fused, twol = _caches(dev, gen, kind, B, cap)
+    q = torch.randn((B, H * G, 1, D), generator=gen).to(torch.bfloat16).to(dev)
+    kn = torch.randn((B, H, 1, D), generator=gen).to(torch.bfloat16).to(dev)
+    vn = torch.randn((B, H, 1, D), generator=gen).to(torch.bfloat16).to(dev)
+    pos_f = torch.tensor(lens, dtype=torch.int32, device=dev)
+    pos_t = pos_f.clone()
+    scale = D ** -0.5
+    ws = torch.zeros(ops.decode_plan(fused.k.dtype, B, H * G, H, D, cap, 16 if fused.paged else 0).workspace_bytes,
+                     dtype=torch.uint8, device=dev)
+    out_f = ops.decode_attention_append(q, fused, kn, vn, pos_f, sm_scale=scale, max_seq_len=cap,
+                                        seq_lens_out=pos_f, workspace=ws, status=status)
+    ops.kv_append(twol, kn, vn, pos_t, pos_t)
+    out_t = ops.decode_attention(q, twol, sm_scale=scale, seq_lens=pos_t, max_seq_len=cap, workspace=ws)
+    torch.cuda.synchronize()
+    new_lens = [L + 1 for L in lens]
+    assert pos_f.cpu().tolist() == new_lens
+    assert pos_t.cpu().tolist() == new_lens
+    assert int(ws[:COUNTER_BYTES].count_nonzero()) == 0
+    assert int(status.item()) == 0
+    assert torch.equal(fused.k.cpu().view(torch.uint8), twol.k.cpu().view(torch.uint8))
+    assert torch.equal(fused.v.cpu().view(torch.uint8), twol.v.cpu().view(torch.uint8))
+    assert torch.equal(out_f.cpu().view(torch.int16), out_t.cpu().view(torch.int16))
+
+    if fused.paged:
+        deq_k = ref.fp8_dequantize_rows(fused.k.cpu(), fused.k_scale.cpu())
+        deq_v = ref.fp8_dequantize_rows(fused.v.cpu(), fused.v_scale.cpu())
+        ks = ref.paged_gather(deq_k, fused.block_table.cpu(), new_lens)
+        vs = ref.paged_gather(deq_v, fused.block_table.cpu(), new_lens)
+        qq = q.cpu().float()
+    else:
+        ks = [fused.k[b, :, :L].cpu() for b, L in enumerate(new_lens)]
+        vs = [fused.v[b, :, :L].cpu() for b, L in enumerate(new_lens)]
+        qq = q.cpu()
+    expect = ref.ragged_decode(qq, ks, vs, scale, G).float()
+    atol = 6e-2 if fused.paged else 2e-2
+    torch.testing.assert_close(out_f.float().cpu(), expect, atol=atol, rtol=1e-2)
+
+
+def test_ordered_rows_replayed_graph_bumps_every_step(dev, status):
+    """A captured fused step of a ragged batch replayed several times, the lengths bumped by each replay: after
+    every replay each row has grown by one and its output matches the oracle over the rows written so far."""
+    gen = torch.Generator().manual_seed(977)
+    B, cap, steps = 48, 700, 4
+    lens = torch.randint(1, 600, (B,), generator=gen).tolist()
+    view, _ = _caches(dev, gen, "bf16", B, cap)
+    q = torch.randn((B, H * G, 1, D), generator=gen).to(torch.bfloat16).to(dev)
+    kn = torch.randn((B, H, 1, D), generator=gen).to(torch.bfloat16).to(dev)
+    vn = torch.randn((B, H, 1, D), generator=gen).to(torch.bfloat16).to(dev)
+    pos = torch.tensor(lens, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    ws = torch.zeros(ops.decode_plan(torch.bfloat16, B, H * G, H, D, cap).workspace_bytes, dtype=torch.uint8,
+                     device=dev)
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        warm = pos.clone()  # an eager launch first (it writes the same rows the first replay writes)
+        ops.decode_attention_append(q, view, kn, vn, warm, sm_scale=D ** -0.5, max_seq_len=cap, seq_lens_out=warm,
+                                    out=out, workspace=ws, status=status)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            ops.decode_attention_append(q, view, kn, vn, pos, sm_scale=D ** -0.5, max_seq_len=cap,
+                                        seq_lens_out=pos, out=out, workspace=ws, status=status)
+        for step in range(steps):
+            graph.replay()
+            torch.cuda.synchronize()
+            now = [L + step + 1 for L in lens]
+            assert pos.cpu().tolist() == now, step
+            ks = [view.k[b, :, :L].cpu() for b, L in enumerate(now)]
+            vs = [view.v[b, :, :L].cpu() for b, L in enumerate(now)]
+            expect = ref.ragged_decode(q.cpu(), ks, vs, D ** -0.5, G).float()
+            torch.testing.assert_close(out.float().cpu(), expect, atol=2e-2, rtol=1e-2)
+    assert int(ws[:COUNTER_BYTES].count_nonzero()) == 0
+    assert int(status.item()) == 0
