@@ -77,8 +77,8 @@ struct DecodeParams {
   int32_t* ws_counter; // [B * Hkv] split arrivals, zero between launches
   int32_t* ws_arrive;  // [B * arrive_stride] APPEND: readers of positions[b], zero between launches
   int32_t arrive_stride;  // int32 slots between batch rows' counters (32: one 128-byte line each)
-  int32_t order_rows;     // nonzero: grid slot z takes the batch row of rank z by length (longest first); needs
-                          // seq_lens and B <= kBlockThreads
+  int32_t order_rows;     // nonzero: grid slots take the batch rows in folded length order (see the kernel);
+                          // needs seq_lens and B <= kBlockThreads
   int32_t* status;
   // APPEND only
   const void* k_new;
@@ -223,13 +223,17 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   const int split = blockIdx.x;
   const int kvh = blockIdx.y;
   const int tid = threadIdx.x;
-  // Row order (ragged batches): grid slot z takes the batch row of rank z in decreasing length (ties in row order),
-  // so that rows of similar length are dispatched together. Every workgroup reads all the lengths and ranks them
-  // the same way (none is bumped before every workgroup has counted in, see count_in), so the slots cover every
-  // row exactly once.
+  // Row order (ragged batches): the rows ranked by decreasing length (ties in row order) are folded over the grid:
+  // slot z < h = ceil(B / 2) takes rank z and slot h + i takes rank B - 1 - i, so that the longest rows go out
+  // first, each with a short row h slots later — the grid's workgroups that share a compute unit then carry
+  // about equal work. Every workgroup reads all the lengths and ranks them the same way (none is bumped before
+  // every workgroup has counted in, see count_in), so the slots cover every row exactly once.
   int b = blockIdx.z;
   if (p.order_rows) {
     const int nb = gridDim.z;
+    const int z = blockIdx.z;
+    const int h = (nb + 1) / 2;
+    const int want = z < h ? z : nb - 1 - (z - h);
     const int len_t = tid < nb ? p.seq_lens[tid] : 0;
     s_row_len[tid] = len_t;
     __syncthreads();
@@ -239,7 +243,7 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
         const int len_j = s_row_len[j];
         rank += (len_j > len_t || (len_j == len_t && j < tid)) ? 1 : 0;
       }
-      if (rank == static_cast<int>(blockIdx.z)) s_row = tid;
+      if (rank == want) s_row = tid;
     }
     __syncthreads();
     b = __builtin_amdgcn_readfirstlane(s_row);

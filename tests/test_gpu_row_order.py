@@ -1,9 +1,9 @@
-"""Ragged batches with many (batch row, kv head) pairs are dispatched longest first.
+"""Ragged batches with many (batch row, kv head) pairs are dispatched in folded length order.
 
 When a launch has more pairs than 3/4 of the compute units, device lengths and at most 256 batch rows, every
-workgroup reads all the rows' lengths, ranks them (decreasing length, ties in row order) and takes the row whose
-rank is its grid slot; the fused append's length bump then waits for every workgroup of the launch, not only
-those of the row. The order may change the timing only: the fused launch must still equal the append followed
+workgroup reads all the rows' lengths, ranks them (decreasing length, ties in row order) and takes the row that
+its grid slot folds to (slot z < ceil(B/2): rank z; slot ceil(B/2) + i: rank B - 1 - i); the fused append's length
+bump then waits for every workgroup of the launch, not only those of the row. The order may change the timing only: the fused launch must still equal the append followed
 by the plain decode bit for bit, cover every row (ties and empty sequences included), bump every length by one,
 leave the workspace counters at zero and match the oracle. 257 rows take the natural order.
 """
