@@ -212,6 +212,7 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   __shared__ int32_t s_last;
   // order_rows: every batch row's length as read at the start (APPEND: before any bump), and this slot's row
   __shared__ int32_t s_row_len[kBlockThreads];
+  __shared__ __align__(16) uint32_t s_row_key[kBlockThreads];
   __shared__ int32_t s_row;
   __shared__ int32_t s_bump;
   // APPEND: the new token's rows as the attention must see them (dequantised codes for fp8 caches)
@@ -236,12 +237,21 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
     const int want = z < h ? z : nb - 1 - (z - h);
     const int len_t = tid < nb ? p.seq_lens[tid] : 0;
     s_row_len[tid] = len_t;
+    // one 32-bit key per row, distinct and ordered like (length, -row): the length clamped to [0, 2^23) (lengths
+    // outside it are clamped by the kernel anyway), then 255 - row; the rows past nb hold 0, below every key
+    // they are compared with. A row's rank is the number of larger keys.
+    const uint32_t key_t = tid < nb ? (static_cast<uint32_t>(min(max(len_t, 0), (1 << 23) - 1)) << 8) |
+                                          static_cast<uint32_t>(255 - tid)
+                                    : 0u;
+    s_row_key[tid] = key_t;
     __syncthreads();
     if (tid < nb) {
       int rank = 0;
-      for (int j = 0; j < nb; ++j) {
-        const int len_j = s_row_len[j];
-        rank += (len_j > len_t || (len_j == len_t && j < tid)) ? 1 : 0;
+      const uint4* keys = reinterpret_cast<const uint4*>(s_row_key);
+#pragma unroll 4
+      for (int j = 0; j < (nb + 3) / 4; ++j) {
+        const uint4 k4 = keys[j];
+        rank += (k4.x > key_t ? 1 : 0) + (k4.y > key_t ? 1 : 0) + (k4.z > key_t ? 1 : 0) + (k4.w > key_t ? 1 : 0);
       }
       if (rank == want) s_row = tid;
     }
