@@ -617,24 +617,30 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
 #pragma unroll
     for (int u = 0; u < U; u += 2) {
       // a masked row's weight is 0, but its registers hold stale words that must not reach the product as NaN/Inf
-      uint32_t va[VEC / 2], vb[VEC / 2];
       const uint32_t wa[4] = {c.ok[u] ? c.v[u].x : 0u, c.ok[u] ? c.v[u].y : 0u, c.ok[u] ? c.v[u].z : 0u,
                               c.ok[u] ? c.v[u].w : 0u};
       const uint32_t wb[4] = {c.ok[u + 1] ? c.v[u + 1].x : 0u, c.ok[u + 1] ? c.v[u + 1].y : 0u,
                               c.ok[u + 1] ? c.v[u + 1].z : 0u, c.ok[u + 1] ? c.v[u + 1].w : 0u};
+      // xs[j] / ys[j]: elements 2j / 2j + 1 of both tokens as a pair of q's 16-bit type (token u in the low half)
+      uint32_t xs[VEC / 2], ys[VEC / 2];
       if constexpr (!FP8) {
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-          va[w] = wa[w];
-          vb[w] = wb[w];
+          xs[w] = __builtin_amdgcn_perm(wb[w], wa[w], 0x05040100u);
+          ys[w] = __builtin_amdgcn_perm(wb[w], wa[w], 0x07060302u);
         }
       } else {
+        // the two tokens' codes interleaved first ([a0, b0, a1, b1] and [a2, b2, a3, b3] of codes 4w .. 4w + 3),
+        // so that each conversion yields one pair: 2 byte permutes and 4 conversions per word pair instead of
+        // 4 conversions and 4 permutes of the converted halves
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-          va[2 * w] = e4m3x2_to_16<Q_DT, false>(wa[w]);
-          va[2 * w + 1] = e4m3x2_to_16<Q_DT, true>(wa[w]);
-          vb[2 * w] = e4m3x2_to_16<Q_DT, false>(wb[w]);
-          vb[2 * w + 1] = e4m3x2_to_16<Q_DT, true>(wb[w]);
+          const uint32_t lo = __builtin_amdgcn_perm(wb[w], wa[w], 0x05010400u);
+          const uint32_t hi = __builtin_amdgcn_perm(wb[w], wa[w], 0x07030602u);
+          xs[2 * w] = e4m3x2_to_16<Q_DT, false>(lo);
+          ys[2 * w] = e4m3x2_to_16<Q_DT, true>(lo);
+          xs[2 * w + 1] = e4m3x2_to_16<Q_DT, false>(hi);
+          ys[2 * w + 1] = e4m3x2_to_16<Q_DT, true>(hi);
         }
       }
       uint32_t pp[G];
@@ -650,12 +656,10 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
       }
 #pragma unroll
       for (int j = 0; j < VEC / 2; ++j) {
-        const uint32_t x = __builtin_amdgcn_perm(vb[j], va[j], 0x05040100u);  // element 2j of both tokens
-        const uint32_t y = __builtin_amdgcn_perm(vb[j], va[j], 0x07060302u);  // element 2j + 1
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-          acc[h][2 * j] = dot2<Q_DT>(x, pp[h], acc[h][2 * j]);
-          acc[h][2 * j + 1] = dot2<Q_DT>(y, pp[h], acc[h][2 * j + 1]);
+          acc[h][2 * j] = dot2<Q_DT>(xs[j], pp[h], acc[h][2 * j]);
+          acc[h][2 * j + 1] = dot2<Q_DT>(ys[j], pp[h], acc[h][2 * j + 1]);
         }
       }
     }
