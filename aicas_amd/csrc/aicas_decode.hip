@@ -432,6 +432,14 @@ int decode_append(const aicas_kv_cache_t* cache, const aicas_qk_prologue_t* pro,
       (v_stride_h % 8))
     return fail(AICAS_ERR_INVALID, "new K/V rows must be 16-byte aligned with strides that are multiples of 8");
   if (max_seq_len < 1) return fail(AICAS_ERR_INVALID, "max_seq_len must count the appended token");
+  if (seq_lens_out && seq_lens_out != positions && batch > 0) {
+    // the bump is stored once every reader of the lengths it replaces is done: only the same array is safe
+    const auto pos = reinterpret_cast<uintptr_t>(positions);
+    const auto out = reinterpret_cast<uintptr_t>(seq_lens_out);
+    const uintptr_t bytes = static_cast<uintptr_t>(batch) * sizeof(int32_t);
+    if (out < pos + bytes && pos < out + bytes)
+      return fail(AICAS_ERR_INVALID, "seq_lens_out may be positions itself but must not otherwise overlap it");
+  }
   DecodeCall c{};
   c.cache = cache;
   c.q_dtype = q_dtype;

@@ -169,8 +169,8 @@ int aicas_decode_attention(const aicas_kv_cache_t* cache, int32_t q_dtype, const
  * positions[b] of the cache exactly as aicas_kv_append would write them (fp8 caches quantize on write), and
  * the attention runs over L_b = positions[b] + 1 tokens, the new one included, with the result
  * aicas_kv_append followed by aicas_decode_attention would give. If seq_lens_out is not NULL,
- * seq_lens_out[b] = positions[b] + 1 is stored once every workgroup has read positions[b]; it may alias
- * positions. max_seq_len must bound positions[b] + 1; min_len (0 if unknown) is a lower bound on every
+ * seq_lens_out[b] = positions[b] + 1 is stored once every workgroup has read positions[b]; it may be
+ * positions itself, but no other overlap with positions is accepted (AICAS_ERR_INVALID). max_seq_len must bound positions[b] + 1; min_len (0 if unknown) is a lower bound on every
  * positions[b], used as by aicas_decode_attention. A token with no slot left in the cache is dropped and
  * AICAS_STATUS_APPEND_OVERFLOW is set. The workspace must come from aicas_decode_plan with the same shapes.
  * Replaces the pair Qwen3VLTextAttention.forward issues per layer and step

@@ -231,6 +231,11 @@ def test_fused_entry_argument_errors():
         ctypes.byref(d), _lib.DTYPE_BF16, FAKE, 16 * 128, 128, None, 8 * 128, 128, FAKE, 8 * 128, 128,
         FAKE + 4096, 16 * 128, 128, FAKE, None, 0, 10, 1, 16, 8, 128, 0.1, 0, FAKE, 1 << 20, None, None)
     assert rc == _lib.ERR_INVALID and "k_new" in _last_error()
+    # seq_lens_out may be positions itself, never a shifted view of it
+    rc = lib.aicas_decode_attention_append(
+        ctypes.byref(d), _lib.DTYPE_BF16, FAKE, 16 * 128, 128, FAKE, 8 * 128, 128, FAKE, 8 * 128, 128,
+        FAKE + 4096, 16 * 128, 128, FAKE + 256, FAKE + 260, 0, 10, 2, 16, 8, 128, 0.1, 0, FAKE, 1 << 20, None, None)
+    assert rc == _lib.ERR_INVALID and "overlap" in _last_error()
 
 
 @no_gpu_only
