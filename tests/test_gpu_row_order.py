@@ -119,3 +119,52 @@ def test_ordered_rows_replayed_graph_bumps_every_step(dev, status):
             torch.testing.assert_close(out.float().cpu(), expect, atol=2e-2, rtol=1e-2)
     assert int(ws[:COUNTER_BYTES].count_nonzero()) == 0
     assert int(status.item()) == 0
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_ordered_rows_random_shapes(dev, status, seed):
+    """Seeded random ragged batches that take the row order (25..256 rows of 8 kv heads): bf16, fp16 or paged
+    fp8, lengths with ties and empty sequences, the plain decode and the fused launch; the fused launch equals
+    the append followed by the plain decode bit for bit, and both match the oracle."""
+    gen = torch.Generator().manual_seed(5000 + seed)
+    B = int(torch.randint(25, 257, (1,), generator=gen))
+    kind = ("bf16", "fp16", "fp8_paged")[seed % 3]
+    cap = 512
+    lens = torch.randint(0, cap - 8, (B,), generator=gen).tolist()
+    for i in range(0, B, 5):
+        lens[i] = lens[(i * 7) % B]  # repeated lengths
+    lens[-1] = 0
+    dt = torch.float16 if kind == "fp16" else torch.bfloat16
+    if kind == "fp8_paged":
+        fused, twol = _caches(dev, gen, kind, B, cap)
+    else:
+        k = torch.randn((B, H, cap, D), generator=gen).to(dt)
+        v = torch.randn((B, H, cap, D), generator=gen).to(dt)
+        fused, twol = [ops.KVCacheView(k.clone().to(dev), v.clone().to(dev)) for _ in range(2)]
+    q = torch.randn((B, H * G, 1, D), generator=gen).to(dt).to(dev)
+    kn = torch.randn((B, H, 1, D), generator=gen).to(dt).to(dev)
+    vn = torch.randn((B, H, 1, D), generator=gen).to(dt).to(dev)
+    pos_f = torch.tensor(lens, dtype=torch.int32, device=dev)
+    pos_t = pos_f.clone()
+    scale = D ** -0.5
+    out_f = ops.decode_attention_append(q, fused, kn, vn, pos_f, sm_scale=scale, max_seq_len=cap,
+                                        seq_lens_out=pos_f, status=status)
+    ops.kv_append(twol, kn, vn, pos_t, pos_t)
+    out_t = ops.decode_attention(q, twol, sm_scale=scale, seq_lens=pos_t, max_seq_len=cap, status=status)
+    torch.cuda.synchronize()
+    new_lens = [L + 1 for L in lens]
+    assert pos_f.cpu().tolist() == new_lens and pos_t.cpu().tolist() == new_lens
+    assert int(status.item()) == 0
+    assert torch.equal(out_f.cpu().view(torch.int16), out_t.cpu().view(torch.int16))
+    if fused.paged:
+        deq_k = ref.fp8_dequantize_rows(fused.k.cpu(), fused.k_scale.cpu())
+        deq_v = ref.fp8_dequantize_rows(fused.v.cpu(), fused.v_scale.cpu())
+        ks = ref.paged_gather(deq_k, fused.block_table.cpu(), new_lens)
+        vs = ref.paged_gather(deq_v, fused.block_table.cpu(), new_lens)
+        qq, atol = q.cpu().float(), 6e-2
+    else:
+        ks = [fused.k[b, :, :L].cpu() for b, L in enumerate(new_lens)]
+        vs = [fused.v[b, :, :L].cpu() for b, L in enumerate(new_lens)]
+        qq, atol = q.cpu(), 2e-2
+    expect = ref.ragged_decode(qq, ks, vs, scale, G).float()
+    torch.testing.assert_close(out_f.float().cpu(), expect, atol=atol, rtol=1e-2)
