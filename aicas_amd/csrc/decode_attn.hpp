@@ -74,7 +74,8 @@ struct DecodeParams {
   float scale_log2;    // sm_scale * log2(e)
   float* ws_ml;        // [B * Hq * max_splits][2]  (m, l)
   float* ws_acc;       // [B * Hq * max_splits][D]
-  int32_t* ws_counter; // [B * Hkv] split arrivals, zero between launches
+  int32_t* ws_counter; // [B * Hkv * counter_stride] split arrivals, zero between launches
+  int32_t counter_stride;  // int32 slots between (batch row, kv head) arrival counters (32: one 128-byte line each)
   int32_t* ws_arrive;  // [B * arrive_stride] APPEND: readers of positions[b], zero between launches
   int32_t arrive_stride;  // int32 slots between batch rows' counters (32: one 128-byte line each)
   int32_t order_rows;     // nonzero: grid slots take the batch rows in folded length order (see the kernel);
@@ -929,7 +930,7 @@ __global__ __launch_bounds__(kBlockThreads) void decode_attn_kernel(DecodeParams
   }
   wait_vmem();
   __syncthreads();
-  int32_t* const counter = p.ws_counter + static_cast<int64_t>(b) * p.num_kv_heads + kvh;
+  int32_t* const counter = p.ws_counter + (static_cast<int64_t>(b) * p.num_kv_heads + kvh) * p.counter_stride;
   if (tid == 0) {
     const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = (prev == n_active - 1) ? 1 : 0;
