@@ -168,3 +168,33 @@ def test_ordered_rows_random_shapes(dev, status, seed):
         qq, atol = q.cpu(), 2e-2
     expect = ref.ragged_decode(qq, ks, vs, scale, G).float()
     torch.testing.assert_close(out_f.float().cpu(), expect, atol=atol, rtol=1e-2)
+
+
+def test_ordered_rows_few_rows_many_heads(dev, status):
+    """Three rows of 96 kv heads (288 pairs, so the row order applies), head_dim 64, lengths 300 / 0 / 5: the
+    fused launch against the two-launch path bit for bit and against the oracle."""
+    gen = torch.Generator().manual_seed(4242)
+    B, Hkv, Gq, Dh, cap = 3, 96, 2, 64, 320
+    lens = [300, 0, 5]
+    k = torch.randn((B, Hkv, cap, Dh), generator=gen).to(torch.bfloat16)
+    v = torch.randn((B, Hkv, cap, Dh), generator=gen).to(torch.bfloat16)
+    fused, twol = [ops.KVCacheView(k.clone().to(dev), v.clone().to(dev)) for _ in range(2)]
+    q = torch.randn((B, Hkv * Gq, 1, Dh), generator=gen).to(torch.bfloat16).to(dev)
+    kn = torch.randn((B, Hkv, 1, Dh), generator=gen).to(torch.bfloat16).to(dev)
+    vn = torch.randn((B, Hkv, 1, Dh), generator=gen).to(torch.bfloat16).to(dev)
+    pos_f = torch.tensor(lens, dtype=torch.int32, device=dev)
+    pos_t = pos_f.clone()
+    scale = Dh ** -0.5
+    out_f = ops.decode_attention_append(q, fused, kn, vn, pos_f, sm_scale=scale, max_seq_len=cap,
+                                        seq_lens_out=pos_f, status=status)
+    ops.kv_append(twol, kn, vn, pos_t, pos_t)
+    out_t = ops.decode_attention(q, twol, sm_scale=scale, seq_lens=pos_t, max_seq_len=cap, status=status)
+    torch.cuda.synchronize()
+    new_lens = [L + 1 for L in lens]
+    assert pos_f.cpu().tolist() == new_lens and pos_t.cpu().tolist() == new_lens
+    assert int(status.item()) == 0
+    assert torch.equal(out_f.cpu().view(torch.int16), out_t.cpu().view(torch.int16))
+    ks = [fused.k[b, :, :L].cpu() for b, L in enumerate(new_lens)]
+    vs = [fused.v[b, :, :L].cpu() for b, L in enumerate(new_lens)]
+    expect = ref.ragged_decode(q.cpu(), ks, vs, scale, Gq).float()
+    torch.testing.assert_close(out_f.float().cpu(), expect, atol=2e-2, rtol=1e-2)
