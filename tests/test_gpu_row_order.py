@@ -198,3 +198,49 @@ def test_ordered_rows_few_rows_many_heads(dev, status):
     vs = [fused.v[b, :, :L].cpu() for b, L in enumerate(new_lens)]
     expect = ref.ragged_decode(q.cpu(), ks, vs, scale, Gq).float()
     torch.testing.assert_close(out_f.float().cpu(), expect, atol=2e-2, rtol=1e-2)
+
+
+def test_ordered_rows_replay_soak(dev, status):
+    """A correctness soak (not aimed at any known failure) of the launch-wide reader count: a ragged fused step
+    (64 rows of 8 kv heads, lengths U{1..400}) captured once and replayed 150 times, lengths bumped by every
+    replay; every length has grown by exactly the number of replays, the counters are zero, and the plain decode
+    over the final cache, in row order too, replayed 50 times, gives the same bits every time."""
+    gen = torch.Generator().manual_seed(808)
+    B, cap, n = 64, 600, 150
+    lens = torch.randint(1, 400, (B,), generator=gen).tolist()
+    view, _ = _caches(dev, gen, "bf16", B, cap)
+    q = torch.randn((B, H * G, 1, D), generator=gen).to(torch.bfloat16).to(dev)
+    kn = torch.randn((B, H, 1, D), generator=gen).to(torch.bfloat16).to(dev)
+    vn = torch.randn((B, H, 1, D), generator=gen).to(torch.bfloat16).to(dev)
+    pos = torch.tensor(lens, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    ws = torch.zeros(ops.decode_plan(torch.bfloat16, B, H * G, H, D, cap).workspace_bytes, dtype=torch.uint8,
+                     device=dev)
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        warm = pos.clone()
+        ops.decode_attention_append(q, view, kn, vn, warm, sm_scale=D ** -0.5, max_seq_len=cap, seq_lens_out=warm,
+                                    out=out, workspace=ws, status=status)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            ops.decode_attention_append(q, view, kn, vn, pos, sm_scale=D ** -0.5, max_seq_len=cap,
+                                        seq_lens_out=pos, out=out, workspace=ws, status=status)
+        for _ in range(n):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert pos.cpu().tolist() == [L + n for L in lens]
+        assert int(ws[:COUNTER_BYTES].count_nonzero()) == 0
+        assert int(status.item()) == 0
+        plain = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(plain, stream=stream):
+            ops.decode_attention(q, view, sm_scale=D ** -0.5, seq_lens=pos, max_seq_len=cap, out=out, workspace=ws,
+                                 status=status)
+        hist = torch.empty((50,) + tuple(q.shape), dtype=q.dtype, device=dev)
+        for i in range(50):
+            plain.replay()
+            hist[i].copy_(out)
+        torch.cuda.synchronize()
+    for i in range(1, 50):
+        assert torch.equal(hist[i].view(torch.int16), hist[0].view(torch.int16)), f"replay {i} differs"
+    assert int(ws[:COUNTER_BYTES].count_nonzero()) == 0
