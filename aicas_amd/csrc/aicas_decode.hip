@@ -259,7 +259,12 @@ int plan(int32_t kv_dtype, int32_t batch, int32_t num_q_heads, int32_t num_kv_he
       // number of splits whatever the bound, and each takes min(splits, ceil(L / minimum split)) from its own
       // length: a launch sized for a loose bound (a graph captured at the cache capacity) runs the grid a tight
       // bound would give.
-      splits_wanted = std::max<int64_t>(1, std::min(splits_wanted, cus / pairs));
+      // At most 4 pairs (one or two sequences with few kv heads): 64 splits per pair, one workgroup per CU at 4
+      // pairs; more splits make the many-way merge the cost, fewer leave CUs idle. Measured on MI355X, bf16,
+      // D=128, us per launch, plan (7/8 per CU) against 64: 1 pair L=32768 15.4 (224) / 11.4, L=16384 10.5
+      // (128) / 9.1; 2 pairs L=16384 11.4 (112) / 9.5; 4 pairs L=32768 16.3 (56) / 15.8, L=8192 9.6 / 9.0.
+      splits_wanted = pairs <= 4 ? std::min<int64_t>(64, cus / pairs) : std::min(splits_wanted, cus / pairs);
+      splits_wanted = std::max<int64_t>(1, splits_wanted);
       tps = 2 * tpi;
       splits = std::min(splits_wanted, ceil_div(bound, tps));
       if (cap >= tpi) splits = std::max(splits, ceil_div(bound, cap));

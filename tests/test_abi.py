@@ -96,11 +96,15 @@ def test_plan_covers_every_token(B, Hkv, L):
 @pytest.mark.skipif(__import__("torch").cuda.is_available(), reason="pins the plan for 256 compute units")
 def test_plan_split_counts():
     """The planner's measured choices for 256 compute units: with few (batch, kv head) pairs about 7/8 of a
-    workgroup per CU and never more than one, with many pairs 7/4, and at least one super-chunk per wave."""
+    workgroup per CU and never more than one (64 splits per pair for at most 4 pairs), with many pairs 7/4, and at
+    least one super-chunk per wave."""
     bf, f8 = _lib.DTYPE_BF16, _lib.DTYPE_FP8_E4M3
     assert _plan(bf, 8, 16, 8, 128, 2176)[2] == 4      # B=8 L=2048 + 128 steps: 256 workgroups
     assert _plan(bf, 1, 16, 8, 128, 32832)[2] == 28    # B=1 L=32768 + 64 steps: 224 workgroups
     assert _plan(bf, 1, 16, 8, 128, 1025)[1:3] == (128, 9)  # B=1 L=1024: 128 tokens = 4 waves x 32
+    # at most 4 pairs: 64 splits per pair once the sequence is long enough (1, 2 and 4 kv heads)
+    assert _plan(bf, 1, 2, 1, 128, 32768)[2] == _plan(bf, 1, 4, 2, 128, 16384)[2] == 64
+    assert _plan(bf, 1, 8, 4, 128, 8192)[2] == 64 and _plan(bf, 1, 8, 4, 128, 4096)[2] == 32
     assert _plan(f8, 32, 16, 8, 128, 8193, 16)[2] == 2  # 256 pairs: 7/4 per CU
     assert _plan(bf, 64, 16, 8, 128, 4097)[2] == 1     # 512 pairs
     # few pairs: the split size is the minimum (two chunks per wave) and the count does not follow a loose bound
