@@ -34,7 +34,8 @@ def _model(dev, vocab):
 
 
 @pytest.mark.parametrize("B, kv_dtype, page_size, block_pool", [
-    (1, None, None, False), (2, None, None, False), (2, torch.float8_e4m3fn, 16, False), (2, None, 4, True)])
+    (1, None, None, False), (2, None, None, False), (2, torch.float8_e4m3fn, 16, False), (2, None, 4, True),
+    (100, None, None, False)])  # 200 (batch row, kv head) pairs: the launches take the row order
 def test_graph_runner_matches_eager_decode(dev, B, kv_dtype, page_size, block_pool):
     from transformers.cache_utils import DynamicCache
 
